@@ -1,0 +1,175 @@
+/*
+ * scriptrs_fe.h -- C ABI of the MI355X log-mel front end.
+ *
+ * This library replaces scriptrs' Parakeet feature extractor
+ * (src/frontend.rs:11-241) and the feature-extraction step of its
+ * long-form chunk workers (src/long_form.rs:266-314, :584-592).
+ * The API is plain C: status codes, plain pointers and sizes.
+ * No Rust, torch or HIP types cross it; a `stream` argument is an opaque
+ * hipStream_t (NULL = the null stream).
+ *
+ * Layout convention (matches the reference's memory order).  The
+ * reference's `extract` returns an Array2<f32> of logical shape [T, 128]
+ * built by `.t().to_owned()` of a [128, T] array (src/frontend.rs:112-115),
+ * whose storage is feature-major.  Every output here is therefore
+ * [feature_size][T] per item.  Item i starts at element
+ * feature_size * frame_offsets[i].
+ *
+ * Threading: one sfe_ctx per host thread.  The reference extractor is
+ * !Sync for the same reason (RefCell workspace, src/frontend.rs:16); calls
+ * on one ctx are serialised by an internal mutex.
+ * Errors: every entry point returns an sfe_status.  sfe_last_error()
+ * returns the calling thread's message for the last failure.
+ */
+#ifndef SCRIPTRS_FE_H
+#define SCRIPTRS_FE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  They map onto the reference's TranscriptionError
+ * (src/error.rs:5-40) as the INTEGRATION notes describe:
+ *   SFE_EMPTY_AUDIO     -> EmptyAudio                  (src/frontend.rs:105-107)
+ *   SFE_AUDIO_TOO_LONG  -> AudioTooLong{..}            (src/pipeline.rs:153-158, :205-210)
+ *   SFE_INVALID_ARG     -> InvalidModelOutput(message)
+ *   SFE_HIP_ERROR       -> InvalidModelOutput(message) (the slot the reference uses
+ *                                                      for "fft failed", src/frontend.rs:82-83) */
+typedef enum sfe_status {
+  SFE_OK = 0,
+  SFE_EMPTY_AUDIO = 1,
+  SFE_INVALID_ARG = 2,
+  SFE_HIP_ERROR = 3,
+  SFE_AUDIO_TOO_LONG = 4
+} sfe_status;
+
+typedef enum sfe_dtype { SFE_F32 = 0, SFE_BF16 = 1 } sfe_dtype;
+
+/* Mirrors TranscriptionConfig (src/config.rs:11-28, defaults :30-44). */
+typedef struct sfe_config {
+  int32_t sample_rate;               /* 16000 */
+  int32_t feature_size;              /* 128   */
+  int32_t n_fft;                     /* 512   */
+  int32_t win_length;                /* 400   */
+  int32_t hop_length;                /* 160   */
+  float preemphasis;                 /* 0.97  */
+  int64_t max_audio_samples;         /* 240000 */
+  int32_t samples_per_encoder_frame; /* 1280  */
+} sfe_config;
+
+/* Mirrors OverlapChunkConfig (src/long_form/planner.rs:85-102). */
+typedef struct sfe_overlap_config {
+  double overlap_seconds;    /* 2.0    */
+  int64_t context_samples;   /* 1280   */
+  int64_t max_model_samples; /* 240000 */
+} sfe_overlap_config;
+
+/* Mirrors ChunkTask for an overlap window (src/long_form.rs:566-582):
+ * the chunk featurized is recording[audio_start, audio_end). */
+typedef struct sfe_chunk {
+  int64_t audio_start;
+  int64_t audio_end;
+  int64_t global_sample_offset;
+  int64_t context_samples;
+} sfe_chunk;
+
+typedef struct sfe_ctx sfe_ctx;
+
+/* ---- host-only helpers (no GPU needed) -------------------------------- */
+
+/* TranscriptionConfig::default() (src/config.rs:30-44). */
+void sfe_config_default(sfe_config* cfg);
+
+/* OverlapChunkConfig::default() (src/long_form/planner.rs:94-102). */
+void sfe_overlap_config_default(sfe_overlap_config* cfg);
+
+/* Frame count of one item: len / hop + 1 (src/frontend.rs:124-127). */
+int64_t sfe_num_frames(const sfe_config* cfg, int64_t len);
+
+/* TranscriptionConfig::max_feature_frames (src/config.rs:50-52). */
+int64_t sfe_max_feature_frames(const sfe_config* cfg);
+
+/* Fast-mode long-form plan: OverlapChunkConfig::plan over [0, audio_len)
+ * (src/long_form/planner.rs:124-137) mapped through push_overlap_task
+ * (src/long_form.rs:566-582), as build_fast_execution_plan does
+ * (src/long_form.rs:439-459).  Writes at most `cap` tasks and sets *n_out
+ * to the full count.  Returns SFE_INVALID_ARG if cap is too small.  The
+ * query pattern (tasks = NULL, cap = 0) also returns SFE_INVALID_ARG
+ * and still sets *n_out. */
+int sfe_plan_fast(const sfe_overlap_config* cfg, int64_t audio_len, sfe_chunk* tasks, int32_t cap,
+                  int32_t* n_out);
+
+/* The host tables the device path uploads.  window[win_length] is
+ * hann_window (src/frontend.rs:161-165).  filterbank is
+ * [feature_size][n_fft/2+1] (src/frontend.rs:188-223).  Both are built
+ * with the reference's f32/f64 operation order.  Either pointer may be
+ * NULL. */
+int sfe_build_tables(const sfe_config* cfg, float* window, float* filterbank);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* sfe_last_error(void);
+
+/* ---- device context ---------------------------------------------------- */
+
+/* ParakeetFeatureExtractor::new (src/frontend.rs:88-102).  Builds the
+ * tables and uploads them to `device`.  The kernels are specialised to
+ * n_fft 512, win 400, hop 160, 128 features; any other shape returns
+ * SFE_INVALID_ARG.  sample_rate and preemphasis are free. */
+int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out);
+void sfe_destroy(sfe_ctx* ctx);
+
+/* ParakeetFeatureExtractor::extract (src/frontend.rs:104-118).  Takes
+ * host audio[len] and writes host out[feature_size * T] (feature-major,
+ * T = len/hop + 1).  Fails with SFE_INVALID_ARG if out_capacity (in floats)
+ * is smaller.  Synchronous.  len == 0 -> SFE_EMPTY_AUDIO.  As in the
+ * reference there is no upper length limit here; that check belongs to
+ * sfe_prepare_chunk. */
+int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64_t out_capacity);
+
+/* ChunkPreparer::prepare / TranscriptionPipeline::prepare_chunk
+ * (src/pipeline.rs:201-216, :145-164).  Checks order: empty ->
+ * SFE_EMPTY_AUDIO; len > cfg.max_audio_samples -> SFE_AUDIO_TOO_LONG; then
+ * sfe_extract.  *feature_frames receives T.  The caller pads to
+ * sfe_max_feature_frames() (PreparedChunk::target_frames). */
+int sfe_prepare_chunk(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64_t out_capacity,
+                      int64_t* feature_frames);
+
+/* Batched extraction of n independent clips from one device buffer.
+ * Clip i is samples[offsets[i], offsets[i+1]).  Dense batches use
+ * offsets[i] = i * L; ragged batches use any non-decreasing offsets.
+ * Each clip is featurized exactly as one extract() call.  samples and out
+ * are device pointers; offsets is host memory with n+1 entries.
+ * frame_offsets (host, n+1 entries) receives the prefix sums of T_i.
+ * out receives sum(T_i) * feature_size elements of out_dtype.
+ * Asynchronous on `stream`.  A clip of length 0 -> SFE_EMPTY_AUDIO. */
+int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets, int32_t n, int32_t out_dtype,
+                      void* out, int64_t* frame_offsets, void* stream);
+
+/* Long-form batched extraction: featurizes n overlapping chunk tasks that
+ * all index into one device recording[len], without copying the overlaps.
+ * This replaces the per-task ChunkPreparer::prepare calls of the
+ * long-form workers (src/long_form.rs:584-592).  Preemphasis restarts at
+ * every task's audio_start, as in the reference.  tasks and frame_offsets
+ * are host memory.  Asynchronous on `stream`. */
+int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
+                       int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream);
+
+/* Streaming long-form extraction from HOST memory.  The recording is
+ * copied host->device in windows of at most window_samples samples,
+ * double-buffered on two streams: the copy of window w+1 overlaps the
+ * compute of window w.  Each window carries every task that ends inside
+ * it, plus its left halo.  `out` is a device buffer sized as for
+ * sfe_extract_chunks.  Copies stage through pinned buffers, so `host`
+ * may be pageable.  Synchronous: returns after all work completes.
+ * window_samples must be at least the longest task. */
+int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host_recording, int64_t len, const sfe_chunk* tasks,
+                                int32_t n, int32_t out_dtype, void* out, int64_t* frame_offsets,
+                                int64_t window_samples);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCRIPTRS_FE_H */
