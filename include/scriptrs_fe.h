@@ -168,6 +168,18 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host_recording, int64
                                 int32_t n, int32_t out_dtype, void* out, int64_t* frame_offsets,
                                 int64_t window_samples);
 
+/* ---- instrumentation (no reference counterpart) ----------------------- */
+
+/* Turn per-kernel timing on or off for ctx.  When on, every launch of the
+ * log-mel and normalisation kernels is bracketed by HIP events on the stream
+ * it runs on.  Turning it on or off clears the recorded launches. */
+int sfe_set_timing(sfe_ctx* ctx, int32_t enable);
+
+/* Waits for the recorded launches and returns the summed durations (ms) of
+ * the log-mel and normalisation kernels since the last read.  Clears the
+ * record.  *launches (may be NULL) receives the number of launch pairs. */
+int sfe_get_timing(sfe_ctx* ctx, double* logmel_ms, double* norm_ms, int32_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

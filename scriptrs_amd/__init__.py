@@ -1,0 +1,14 @@
+"""MI355X-native log-mel front end of scriptrs (src/frontend.rs), batched over
+the chunks of its long-form planner (src/long_form).
+
+All feature computation runs in hand-written gfx950 HIP kernels inside
+``libscriptrs_fe.so``, reached through the C ABI in ``include/scriptrs_fe.h``.
+"""
+from .frontend import (  # noqa: F401
+    AudioTooLong, ChunkPreparer, EmptyAudio, InvalidModelOutput, ParakeetFeatureExtractor, PreparedChunk,
+    TranscriptionConfig, TranscriptionError, build_tables, num_frames,
+)
+from .long_form import (  # noqa: F401
+    ChunkTask, LongFormConfig, LongFormFeatures, OverlapChunkConfig, SampleRange, build_fast_execution_plan,
+    featurize_long_form, parallel_worker_count,
+)

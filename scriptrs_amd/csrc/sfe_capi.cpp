@@ -1,0 +1,554 @@
+// C-ABI of the MI355X log-mel front end (declared in include/scriptrs_fe.h).
+//
+// Host responsibilities: argument validation with the reference's error
+// semantics, per-call item tables (one H2D copy from a pinned staging
+// buffer), device buffer management and stream ordering.  All compute runs
+// in the HIP kernels of sfe_kernels.hip; there is no CPU compute path.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/scriptrs_fe.h"
+#include "sfe_internal.hpp"
+
+using sfe::Item;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(SFE_HIP_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define SFE_HIP(call)                             \
+  do {                                            \
+    hipError_t e_ = (call);                       \
+    if (e_ != hipSuccess) return hip_fail(e_, #call); \
+  } while (0)
+
+// Device buffer that grows on demand.  Growth synchronises the device
+// first, so no queued kernel still reads the old allocation.
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  hipError_t reserve(size_t bytes) {
+    if (bytes <= cap) return hipSuccess;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    size_t want = std::max(bytes, cap * 3 / 2);
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+    e = hipMalloc(&ptr, want);
+    if (e == hipSuccess) cap = want;
+    return e;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+};
+
+// Pinned host buffer that grows on demand; `ev` marks the last copy out of it.
+struct PinBuf {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  hipEvent_t ev = nullptr;
+  bool pending = false;
+  hipError_t wait() {
+    if (!pending) return hipSuccess;
+    pending = false;
+    return hipEventSynchronize(ev);
+  }
+  hipError_t reserve(size_t bytes) {
+    hipError_t e = wait();
+    if (e != hipSuccess) return e;
+    if (!ev) {
+      e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+    }
+    if (bytes <= cap) return hipSuccess;
+    if (ptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+    size_t want = std::max(bytes, (size_t)4096);
+    e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
+    if (e == hipSuccess) cap = want;
+    return e;
+  }
+  void release() {
+    if (ptr) (void)hipHostFree(ptr);
+    if (ev) (void)hipEventDestroy(ev);
+    ptr = nullptr;
+    ev = nullptr;
+    cap = 0;
+  }
+};
+
+bool shape_supported(const sfe_config* c, std::string* why) {
+  if (c->n_fft != sfe::kNfft || c->win_length != sfe::kWin || c->hop_length != sfe::kHop ||
+      c->feature_size != sfe::kMel) {
+    *why = "unsupported frontend shape: the kernels are specialised to n_fft=512, win_length=400, "
+           "hop_length=160, feature_size=128";
+    return false;
+  }
+  if (c->sample_rate <= 0) {
+    *why = "sample_rate must be positive";
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+struct sfe_ctx {
+  sfe_config cfg;
+  int device = 0;
+  std::mutex mu;
+  sfe::DevTables* d_tables = nullptr;
+  hipStream_t s_compute = nullptr;  // internal streams, default priority
+  hipStream_t s_copy = nullptr;
+  DevBuf meta;      // Item tables
+  PinBuf h_meta;
+  DevBuf scratch;   // f32 raw log-mel for bf16 output
+  DevBuf io_in;     // sfe_extract staging (audio)
+  DevBuf io_out;    // sfe_extract staging (features)
+  DevBuf win[2];    // streamed windows
+  PinBuf h_win[2];
+  hipEvent_t ev_copied[2] = {nullptr, nullptr};
+  hipEvent_t ev_done[2] = {nullptr, nullptr};
+  // kernel timing (sfe_set_timing): events around each launch, summed on read
+  bool timing = false;
+  std::vector<hipEvent_t> tev;  // pairs: start, end; kind alternates logmel, norm
+  size_t tev_used = 0;
+};
+
+namespace {
+
+// Builds the item table for n spans and returns total tiles.
+int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vector<Item>* items,
+                int64_t* frame_offsets, int64_t* total_tiles) {
+  items->resize(n);
+  int64_t fo = 0, tiles = 0;
+  if (frame_offsets) frame_offsets[0] = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    if (lens[i] <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty (item " + std::to_string(i) + ")");
+    const int64_t T = lens[i] / sfe::kHop + 1;
+    if (T > INT32_MAX / 2) return fail(SFE_INVALID_ARG, "item too long");
+    Item& it = (*items)[i];
+    it.start = starts[i];
+    it.len = lens[i];
+    it.out_off = (int64_t)sfe::kMel * fo;
+    it.T = (int32_t)T;
+    it.tile_off = (int32_t)tiles;
+    fo += T;
+    tiles += sfe::tiles_for(T);
+    if (frame_offsets) frame_offsets[i + 1] = fo;
+  }
+  if (tiles > INT32_MAX) return fail(SFE_INVALID_ARG, "batch too large for one launch");
+  *total_tiles = tiles;
+  return SFE_OK;
+}
+
+hipEvent_t timing_event(sfe_ctx* ctx) {
+  if (ctx->tev_used == ctx->tev.size()) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    ctx->tev.push_back(e);
+  }
+  return ctx->tev[ctx->tev_used++];
+}
+
+// Launches the log-mel kernel then the normalisation kernel; with timing on,
+// brackets each with events (read back by sfe_get_timing).
+int launch_pair(sfe_ctx* ctx, const float* samples, const Item* d_items, int n, int tiles, float* raw, void* out,
+                int32_t out_dtype, hipStream_t stream) {
+  hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
+  if (ctx->timing)
+    for (int i = 0; i < 4; ++i)
+      if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
+  if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
+  SFE_HIP(sfe::launch_logmel(samples, d_items, n, tiles, ctx->d_tables, ctx->cfg.preemphasis, raw, stream));
+  if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
+  if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
+  SFE_HIP(sfe::launch_norm(raw, d_items, n, out, out_dtype == SFE_BF16, stream));
+  if (e[3]) SFE_HIP(hipEventRecord(e[3], stream));
+  return SFE_OK;
+}
+
+// Uploads items through the pinned staging buffer on `stream`, then runs
+// the log-mel and normalisation kernels.
+int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items, int64_t total_tiles,
+              int64_t total_frames, int32_t out_dtype, void* out, hipStream_t stream) {
+  const size_t mbytes = items.size() * sizeof(Item);
+  SFE_HIP(ctx->h_meta.reserve(mbytes));
+  SFE_HIP(ctx->meta.reserve(mbytes));
+  memcpy(ctx->h_meta.ptr, items.data(), mbytes);
+  SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, stream));
+  SFE_HIP(hipEventRecord(ctx->h_meta.ev, stream));
+  ctx->h_meta.pending = true;
+  const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
+  float* raw = static_cast<float*>(out);
+  if (out_dtype == SFE_BF16) {
+    SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
+    raw = static_cast<float*>(ctx->scratch.ptr);
+  }
+  return launch_pair(ctx, samples, d_items, (int)items.size(), (int)total_tiles, raw, out, out_dtype, stream);
+}
+
+int check_ctx(sfe_ctx* ctx) {
+  if (!ctx) return fail(SFE_INVALID_ARG, "null context");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  return SFE_OK;
+}
+
+int check_dtype(int32_t d) {
+  if (d != SFE_F32 && d != SFE_BF16) return fail(SFE_INVALID_ARG, "out_dtype must be SFE_F32 or SFE_BF16");
+  return SFE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void sfe_config_default(sfe_config* c) {
+  c->sample_rate = 16000;
+  c->feature_size = 128;
+  c->n_fft = 512;
+  c->win_length = 400;
+  c->hop_length = 160;
+  c->preemphasis = 0.97f;
+  c->max_audio_samples = 240000;
+  c->samples_per_encoder_frame = 1280;
+}
+
+void sfe_overlap_config_default(sfe_overlap_config* c) {
+  c->overlap_seconds = 2.0;
+  c->context_samples = 1280;
+  c->max_model_samples = 240000;
+}
+
+int64_t sfe_num_frames(const sfe_config* cfg, int64_t len) {
+  const int64_t hop = cfg && cfg->hop_length > 0 ? cfg->hop_length : sfe::kHop;
+  return len < 0 ? 0 : len / hop + 1;
+}
+
+int64_t sfe_max_feature_frames(const sfe_config* cfg) {
+  return cfg->max_audio_samples / cfg->hop_length + 1;
+}
+
+int sfe_plan_fast(const sfe_overlap_config* cfg, int64_t audio_len, sfe_chunk* tasks, int32_t cap,
+                  int32_t* n_out) {
+  if (!cfg || !n_out) return fail(SFE_INVALID_ARG, "null argument");
+  if (audio_len < 0) return fail(SFE_INVALID_ARG, "negative audio length");
+  const int64_t spf = 1280;  // SAMPLES_PER_ENCODER_FRAME, src/constants.rs:4-5
+  const int64_t hop = 160;   // MEL_HOP_SAMPLES
+  auto sat = [](int64_t a, int64_t b) { return a > b ? a - b : (int64_t)0; };
+  // chunk_samples / overlap_samples / stride_samples: src/long_form/planner.rs:105-122
+  int64_t raw = std::max(sat(sat(cfg->max_model_samples, cfg->context_samples), hop), spf);
+  const int64_t chunk = raw / spf * spf;
+  double req_d = cfg->overlap_seconds * 16000.0;
+  int64_t req = req_d != req_d || req_d <= 0.0 ? 0 : (req_d >= 9.2e18 ? INT64_MAX : (int64_t)req_d);
+  const int64_t overlap = std::min(req, chunk / 2) / spf * spf;
+  const int64_t stride = std::max(sat(chunk, overlap), spf) / spf * spf;
+  // plan (planner.rs:124-137) + push_overlap_task (long_form.rs:566-582)
+  int64_t count = 0;
+  int64_t start = 0;
+  while (start < audio_len) {
+    int64_t end = std::min(start + chunk, audio_len);
+    if (tasks && count < cap) {
+      int64_t ctx_start = sat(start, cfg->context_samples);
+      tasks[count] = {ctx_start, end, start, start - ctx_start};
+    }
+    ++count;
+    if (end == audio_len) break;
+    start += stride;
+  }
+  if (count > INT32_MAX) return fail(SFE_INVALID_ARG, "too many tasks");
+  *n_out = (int32_t)count;
+  if (count > cap || (!tasks && count > 0)) return fail(SFE_INVALID_ARG, "task buffer too small");
+  return SFE_OK;
+}
+
+int sfe_build_tables(const sfe_config* cfg, float* window, float* filterbank) {
+  if (!cfg || cfg->win_length <= 1 || cfg->n_fft <= 0 || cfg->feature_size <= 0 || cfg->sample_rate <= 0)
+    return fail(SFE_INVALID_ARG, "invalid config");
+  if (window) sfe::hann_window(cfg->win_length, window);
+  if (filterbank) sfe::mel_filterbank(cfg->n_fft, cfg->feature_size, cfg->sample_rate, filterbank);
+  return SFE_OK;
+}
+
+const char* sfe_last_error(void) { return g_last_error.c_str(); }
+
+int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
+  if (!cfg || !out) return fail(SFE_INVALID_ARG, "null argument");
+  *out = nullptr;
+  std::string why;
+  if (!shape_supported(cfg, &why)) return fail(SFE_INVALID_ARG, why);
+  sfe::DevTables host;
+  if (!sfe::build_dev_tables(cfg->sample_rate, &host))
+    return fail(SFE_INVALID_ARG, "mel filter wider than the kernel's band table");
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess || ndev == 0) return fail(SFE_HIP_ERROR, "no HIP device available");
+  if (device < 0 || device >= ndev) return fail(SFE_INVALID_ARG, "device index out of range");
+  SFE_HIP(hipSetDevice(device));
+  sfe_ctx* ctx = new sfe_ctx();
+  ctx->cfg = *cfg;
+  ctx->device = device;
+  auto cleanup = [&](int rc) {
+    sfe_destroy(ctx);
+    return rc;
+  };
+  if ((e = hipMalloc(&ctx->d_tables, sizeof(sfe::DevTables))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc"));
+  if ((e = hipMemcpy(ctx->d_tables, &host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMemcpy"));
+  if ((e = hipStreamCreateWithFlags(&ctx->s_compute, hipStreamNonBlocking)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipStreamCreate"));
+  if ((e = hipStreamCreateWithFlags(&ctx->s_copy, hipStreamNonBlocking)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipStreamCreate"));
+  for (int i = 0; i < 2; ++i) {
+    if ((e = hipEventCreateWithFlags(&ctx->ev_copied[i], hipEventDisableTiming)) != hipSuccess)
+      return cleanup(hip_fail(e, "hipEventCreate"));
+    if ((e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming)) != hipSuccess)
+      return cleanup(hip_fail(e, "hipEventCreate"));
+  }
+  *out = ctx;
+  return SFE_OK;
+}
+
+void sfe_destroy(sfe_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipDeviceSynchronize();
+  if (ctx->d_tables) (void)hipFree(ctx->d_tables);
+  ctx->meta.release();
+  ctx->h_meta.release();
+  ctx->scratch.release();
+  ctx->io_in.release();
+  ctx->io_out.release();
+  for (int i = 0; i < 2; ++i) {
+    ctx->win[i].release();
+    ctx->h_win[i].release();
+    if (ctx->ev_copied[i]) (void)hipEventDestroy(ctx->ev_copied[i]);
+    if (ctx->ev_done[i]) (void)hipEventDestroy(ctx->ev_done[i]);
+  }
+  for (hipEvent_t e : ctx->tev) (void)hipEventDestroy(e);
+  if (ctx->s_compute) (void)hipStreamDestroy(ctx->s_compute);
+  if (ctx->s_copy) (void)hipStreamDestroy(ctx->s_copy);
+  delete ctx;
+}
+
+int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64_t out_capacity) {
+  if (len <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty");
+  if (!audio || !out) return fail(SFE_INVALID_ARG, "null buffer");
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const int64_t T = len / sfe::kHop + 1;
+  const int64_t nout = T * sfe::kMel;
+  if (out_capacity < nout) return fail(SFE_INVALID_ARG, "output buffer too small");
+  SFE_HIP(ctx->io_in.reserve((size_t)len * sizeof(float)));
+  SFE_HIP(ctx->io_out.reserve((size_t)nout * sizeof(float)));
+  hipStream_t s = ctx->s_compute;
+  SFE_HIP(hipMemcpyAsync(ctx->io_in.ptr, audio, (size_t)len * sizeof(float), hipMemcpyHostToDevice, s));
+  std::vector<Item> items;
+  int64_t start = 0, tiles = 0, fo[2];
+  if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
+  if ((rc = run_items(ctx, static_cast<float*>(ctx->io_in.ptr), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
+    return rc;
+  SFE_HIP(hipMemcpyAsync(out, ctx->io_out.ptr, (size_t)nout * sizeof(float), hipMemcpyDeviceToHost, s));
+  SFE_HIP(hipStreamSynchronize(s));
+  return SFE_OK;
+}
+
+int sfe_prepare_chunk(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64_t out_capacity,
+                      int64_t* feature_frames) {
+  if (len <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty");
+  if (!ctx) return fail(SFE_INVALID_ARG, "null context");
+  if (len > ctx->cfg.max_audio_samples) {
+    char buf[160];
+    snprintf(buf, sizeof buf, "audio exceeds the single-chunk limit: actual=%.2fs max=%.2fs",
+             (double)len / ctx->cfg.sample_rate, (double)ctx->cfg.max_audio_samples / ctx->cfg.sample_rate);
+    return fail(SFE_AUDIO_TOO_LONG, buf);
+  }
+  int rc = sfe_extract(ctx, audio, len, out, out_capacity);
+  if (rc == SFE_OK && feature_frames) *feature_frames = len / sfe::kHop + 1;
+  return rc;
+}
+
+int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets, int32_t n, int32_t out_dtype,
+                      void* out, int64_t* frame_offsets, void* stream) {
+  if (n <= 0 || !offsets || !samples || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid batch arguments");
+  int rc = check_dtype(out_dtype);
+  if (rc) return rc;
+  std::vector<int64_t> starts(n), lens(n);
+  for (int32_t i = 0; i < n; ++i) {
+    if (offsets[i + 1] < offsets[i] || offsets[i] < 0)
+      return fail(SFE_INVALID_ARG, "offsets must be non-negative and non-decreasing");
+    starts[i] = offsets[i];
+    lens[i] = offsets[i + 1] - offsets[i];
+  }
+  if ((rc = check_ctx(ctx))) return rc;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  std::vector<Item> items;
+  int64_t tiles = 0;
+  if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
+  return run_items(ctx, samples, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+}
+
+int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
+                       int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream) {
+  if (n <= 0 || !tasks || !recording || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+  int rc = check_dtype(out_dtype);
+  if (rc) return rc;
+  std::vector<int64_t> starts(n), lens(n);
+  for (int32_t i = 0; i < n; ++i) {
+    const sfe_chunk& t = tasks[i];
+    if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+      return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+    starts[i] = t.audio_start;
+    lens[i] = t.audio_end - t.audio_start;
+  }
+  if ((rc = check_ctx(ctx))) return rc;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  std::vector<Item> items;
+  int64_t tiles = 0;
+  if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
+  return run_items(ctx, recording, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+}
+
+int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, const sfe_chunk* tasks, int32_t n,
+                                int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples) {
+  if (n <= 0 || !tasks || !host || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+  int rc = check_dtype(out_dtype);
+  if (rc) return rc;
+  std::vector<int64_t> starts(n), lens(n);
+  for (int32_t i = 0; i < n; ++i) {
+    const sfe_chunk& t = tasks[i];
+    if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+      return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+    if (t.audio_end - t.audio_start > window_samples)
+      return fail(SFE_INVALID_ARG, "window_samples is shorter than task " + std::to_string(i));
+    if (i > 0 && t.audio_start < tasks[i - 1].audio_start)
+      return fail(SFE_INVALID_ARG, "tasks must be ordered by audio_start");
+    starts[i] = t.audio_start;
+    lens[i] = t.audio_end - t.audio_start;
+  }
+  if ((rc = check_ctx(ctx))) return rc;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  std::vector<Item> items;
+  int64_t tiles = 0;
+  if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
+
+  // Group tasks into windows [wstart, wend) no longer than window_samples;
+  // items are re-based to the window and their tiles to the group.
+  struct Group {
+    int32_t first, count;
+    int64_t wstart, wend;
+    int32_t tiles;
+  };
+  std::vector<Group> groups;
+  for (int32_t i = 0; i < n;) {
+    Group g{i, 0, items[i].start, items[i].start, 0};
+    while (i < n && items[i].start + items[i].len - g.wstart <= window_samples) {
+      g.wend = std::max(g.wend, items[i].start + items[i].len);
+      ++i;
+      ++g.count;
+    }
+    groups.push_back(g);
+  }
+  for (Group& g : groups) {
+    int32_t t = 0;
+    for (int32_t i = g.first; i < g.first + g.count; ++i) {
+      items[i].start -= g.wstart;
+      items[i].tile_off = t;
+      t += (int32_t)sfe::tiles_for(items[i].T);
+    }
+    g.tiles = t;
+  }
+  const size_t mbytes = items.size() * sizeof(Item);
+  SFE_HIP(ctx->h_meta.reserve(mbytes));
+  SFE_HIP(ctx->meta.reserve(mbytes));
+  float* raw = static_cast<float*>(out);
+  if (out_dtype == SFE_BF16) {
+    SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
+    raw = static_cast<float*>(ctx->scratch.ptr);
+  }
+  for (int b = 0; b < 2; ++b) {
+    SFE_HIP(ctx->win[b].reserve((size_t)window_samples * sizeof(float)));
+    SFE_HIP(ctx->h_win[b].reserve((size_t)window_samples * sizeof(float)));
+  }
+  hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
+  memcpy(ctx->h_meta.ptr, items.data(), mbytes);
+  SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, sc));
+  SFE_HIP(hipEventRecord(ctx->h_meta.ev, sc));
+  ctx->h_meta.pending = true;
+  const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
+  bool used[2] = {false, false};
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const Group& g = groups[gi];
+    const int b = (int)(gi & 1);
+    const size_t bytes = (size_t)(g.wend - g.wstart) * sizeof(float);
+    // the pinned buffer is free once its previous H2D copy has finished
+    SFE_HIP(ctx->h_win[b].wait());
+    memcpy(ctx->h_win[b].ptr, host + g.wstart, bytes);
+    // the device window is free once the kernels that read it have finished
+    if (used[b]) SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_done[b], 0));
+    SFE_HIP(hipMemcpyAsync(ctx->win[b].ptr, ctx->h_win[b].ptr, bytes, hipMemcpyHostToDevice, sx));
+    SFE_HIP(hipEventRecord(ctx->h_win[b].ev, sx));
+    ctx->h_win[b].pending = true;
+    SFE_HIP(hipEventRecord(ctx->ev_copied[b], sx));
+    SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[b], 0));
+    rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), d_items + g.first, g.count, g.tiles, raw, out,
+                     out_dtype, sc);
+    if (rc) return rc;
+    SFE_HIP(hipEventRecord(ctx->ev_done[b], sc));
+    used[b] = true;
+  }
+  SFE_HIP(hipStreamSynchronize(sc));
+  SFE_HIP(hipStreamSynchronize(sx));
+  return SFE_OK;
+}
+
+int sfe_set_timing(sfe_ctx* ctx, int32_t enable) {
+  if (!ctx) return fail(SFE_INVALID_ARG, "null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->timing = enable != 0;
+  ctx->tev_used = 0;
+  return SFE_OK;
+}
+
+int sfe_get_timing(sfe_ctx* ctx, double* logmel_ms, double* norm_ms, int32_t* launches) {
+  if (!ctx || !logmel_ms || !norm_ms) return fail(SFE_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  double a = 0.0, b = 0.0;
+  for (size_t i = 0; i + 3 < ctx->tev_used; i += 4) {
+    float t0 = 0.f, t1 = 0.f;
+    SFE_HIP(hipEventSynchronize(ctx->tev[i + 3]));
+    SFE_HIP(hipEventElapsedTime(&t0, ctx->tev[i], ctx->tev[i + 1]));
+    SFE_HIP(hipEventElapsedTime(&t1, ctx->tev[i + 2], ctx->tev[i + 3]));
+    a += t0;
+    b += t1;
+  }
+  *logmel_ms = a;
+  *norm_ms = b;
+  if (launches) *launches = (int32_t)(ctx->tev_used / 4);
+  ctx->tev_used = 0;
+  return SFE_OK;
+}
+
+}  // extern "C"

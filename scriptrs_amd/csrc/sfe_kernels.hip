@@ -1,0 +1,372 @@
+// CDNA4 (gfx950) kernels of the log-mel front end.
+//
+// sfe_logmel_kernel fuses, per tile of 32 frames of one item, everything
+// ParakeetFeatureExtractor::extract does before normalisation
+// (src/frontend.rs:104-147, :150-159):
+//   preemphasis restarted at the item start -> 256-zero padding ->
+//   400-tap left-aligned Hann window -> 512-point real FFT -> |X|^2 ->
+//   128x257 Slaney mel contraction -> ln(x + 2^-24)
+// and writes the raw log-mel feature-major ([128][T] per item).
+// sfe_norm_kernel then applies normalize_columns (src/frontend.rs:225-241)
+// per (item, feature) row.
+//
+// FFT mapping: the 512-point real FFT is a 256-point complex FFT of
+// z[m] = r[2m] + i r[2m+1] followed by the even/odd split.  The 256-point
+// FFT is 16 x 16: 16 lanes own one frame, each lane holds 16 complex values
+// in VGPRs, runs a 16-point DFT, applies the inter-stage twiddles, the 16x16
+// transpose goes through LDS (row stride 17 complex, conflict-free), and a
+// second 16-point DFT finishes the transform.  A 64-wide wavefront therefore
+// transforms 4 frames at once, and every lane of the wave is busy.
+// The split partner Z[256-k] is fetched with one cross-lane shuffle per
+// value.
+#include <hip/hip_runtime.h>
+
+#include "sfe_internal.hpp"
+
+namespace sfe {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kSigLen = kHop * (kTile - 1) + kWin;  // 5360 preemphasised samples per tile
+constexpr int kXStride = 17;                         // transpose row stride (complex)
+constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
+constexpr int kSlots = 16;                           // 4 waves x 4 frame groups
+constexpr int kLmStride = kTile + 1;
+constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
+// ln(2^-24) rounded to f32, the value the reference's f32 ln returns for a
+// mel value of exactly zero.
+constexpr float kLnGuard = -16.635532333438687f;
+constexpr float kLn2 = 0.69314718055994531f;
+
+struct __align__(8) cf {
+  float x, y;
+};
+
+__device__ __forceinline__ cf cadd(cf a, cf b) { return {a.x + b.x, a.y + b.y}; }
+__device__ __forceinline__ cf csub(cf a, cf b) { return {a.x - b.x, a.y - b.y}; }
+__device__ __forceinline__ cf cmul(cf a, cf w) { return {a.x * w.x - a.y * w.y, a.x * w.y + a.y * w.x}; }
+
+// Multiply by e^{-2 pi i j/16} for a compile-time j.
+template <int J>
+__device__ __forceinline__ cf tw16(cf a) {
+  constexpr float C1 = 0.92387953251128674f;  // cos(pi/8)
+  constexpr float S1 = 0.38268343236508978f;  // sin(pi/8)
+  constexpr float R = 0.70710678118654752f;   // sqrt(1/2)
+  if constexpr (J == 0) return a;
+  else if constexpr (J == 1) return {a.x * C1 + a.y * S1, a.y * C1 - a.x * S1};
+  else if constexpr (J == 2) return {R * (a.x + a.y), R * (a.y - a.x)};
+  else if constexpr (J == 3) return {a.x * S1 + a.y * C1, a.y * S1 - a.x * C1};
+  else if constexpr (J == 4) return {a.y, -a.x};
+  else if constexpr (J == 6) return {R * (a.y - a.x), -R * (a.x + a.y)};
+  else {
+    static_assert(J == 9, "unused twiddle");
+    return {-(a.x * C1 + a.y * S1), -(a.y * C1 - a.x * S1)};
+  }
+}
+
+// 4-point forward DFT in place on (a0, a1, a2, a3); when Z3 the caller
+// guarantees a3 == 0 and it is never read.
+template <bool Z3>
+__device__ __forceinline__ void dft4(cf& a0, cf& a1, cf& a2, cf& a3) {
+  cf t0 = cadd(a0, a2), t1 = csub(a0, a2);
+  cf t2 = Z3 ? a1 : cadd(a1, a3);
+  cf t3 = Z3 ? a1 : csub(a1, a3);
+  a0 = cadd(t0, t2);
+  a2 = csub(t0, t2);
+  a1 = {t1.x + t3.y, t1.y - t3.x};  // t1 - i t3
+  a3 = {t1.x - t3.y, t1.y + t3.x};  // t1 + i t3
+}
+
+// 16-point forward DFT in registers: in a[m] -> out a[k] (natural order).
+// m = p + 4q, k = c + 4d.  PRUNE: a[13], a[14], a[15] are zero.
+template <bool PRUNE>
+__device__ __forceinline__ void dft16(cf (&a)[16]) {
+  // inner 4-point DFTs over q for each p: U[p][c] stored at a[p + 4c]
+  dft4<false>(a[0], a[4], a[8], a[12]);
+  dft4<PRUNE>(a[1], a[5], a[9], a[13]);
+  dft4<PRUNE>(a[2], a[6], a[10], a[14]);
+  dft4<PRUNE>(a[3], a[7], a[11], a[15]);
+  // twiddles e^{-2 pi i p c / 16}
+  a[5] = tw16<1>(a[5]);
+  a[9] = tw16<2>(a[9]);
+  a[13] = tw16<3>(a[13]);
+  a[6] = tw16<2>(a[6]);
+  a[10] = tw16<4>(a[10]);
+  a[14] = tw16<6>(a[14]);
+  a[7] = tw16<3>(a[7]);
+  a[11] = tw16<6>(a[11]);
+  a[15] = tw16<9>(a[15]);
+  // outer 4-point DFTs over p for each c: X[c + 4d] = sum_p V[p][c] W4^{pd}
+  dft4<false>(a[0], a[1], a[2], a[3]);
+  dft4<false>(a[4], a[5], a[6], a[7]);
+  dft4<false>(a[8], a[9], a[10], a[11]);
+  dft4<false>(a[12], a[13], a[14], a[15]);
+  // now X[c + 4d] sits at a[4c + d]: transpose the 4x4 index
+  cf b[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) b[i] = a[i];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) a[c + 4 * d] = b[4 * c + d];
+}
+
+// Orders LDS traffic between the lanes that share a frame slot.  Every wave
+// runs the same number of frame iterations, so a workgroup barrier is safe.
+__device__ __forceinline__ void wave_lds_sync() { __syncthreads(); }
+
+__global__ __launch_bounds__(kThreads) void sfe_logmel_kernel(const float* __restrict__ samples,
+                                                              const Item* __restrict__ items, int n_items,
+                                                              const DevTables* __restrict__ tb, float coef,
+                                                              float* __restrict__ out) {
+  __shared__ __align__(16) float sig[kSigLen];
+  __shared__ __align__(16) cf xch[kSlots * kSlot];
+  __shared__ __align__(16) float lm[kMel * kLmStride];
+  __shared__ __align__(16) float melw[kMel * kMelW];
+  __shared__ int mello[kMel];
+  __shared__ int melcnt[kMel];
+
+  const int tid = threadIdx.x;
+  const int tile = blockIdx.x;
+  int lo = 0, hi = n_items - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (items[mid].tile_off <= tile) lo = mid;
+    else hi = mid - 1;
+  }
+  const Item it = items[lo];
+  const int f0 = (tile - it.tile_off) * kTile;
+  const int nf = min(kTile, it.T - f0);
+  const float* x = samples + it.start;
+  const int64_t L = it.len;
+  const int64_t s0 = (int64_t)f0 * kHop - kPad;
+
+  // Stage the preemphasised, zero-padded signal of the tile:
+  // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
+  // src/frontend.rs:157 computes it), zero outside [0, L).
+  for (int j = tid; j < kSigLen; j += kThreads) {
+    int64_t s = s0 + j;
+    float v = 0.0f;
+    if (s >= 0 && s < L) {
+      float cur = x[s];
+      v = (s == 0) ? cur : __fsub_rn(cur, __fmul_rn(coef, x[s - 1]));
+    }
+    sig[j] = v;
+  }
+  for (int j = tid; j < kMel * kMelW; j += kThreads) melw[j] = tb->mel_w[j];
+  if (tid < kMel) {
+    mello[tid] = tb->mel_lo[tid];
+    melcnt[tid] = tb->mel_cnt[tid];
+  }
+
+  const int lane = tid & 63;
+  const int l = lane & 15;
+  const int slot = (tid >> 6) * 4 + (lane >> 4);
+  const int partner = (16 - l) & 15;
+
+  // Per-lane constants: window taps of this lane's inputs, inter-stage
+  // twiddles e^{-2 pi i l k1/256} and split twiddles e^{-2 pi i k/512}.
+  cf wv[13];
+#pragma unroll
+  for (int m2 = 0; m2 < 13; ++m2) {
+    int n = 2 * l + 32 * m2;  // < 512, taps past 400 are zero
+    wv[m2] = {tb->window[n], tb->window[n + 1]};
+  }
+  cf t256[16];
+#pragma unroll
+  for (int k1 = 0; k1 < 16; ++k1) {
+    // A per-lane table row, indexed affinely: hipcc 7.2 (LLVM 22) miscompiled
+    // the equivalent tw[(l * k1) & 255] gather, loading .y of k1 = 1 from
+    // element 2l.
+    float2 w = tb->tw256[l * 16 + k1];
+    t256[k1] = {w.x, w.y};
+  }
+  cf t512[9];
+#pragma unroll
+  for (int k2 = 0; k2 < 9; ++k2) {
+    float2 w = tb->tw512[l + 16 * k2];
+    t512[k2] = {w.x, w.y};
+  }
+  __syncthreads();
+
+  cf* X = xch + slot * kSlot;
+  float* P = reinterpret_cast<float*>(X);
+  for (int fr = slot; fr < kTile; fr += kSlots) {
+    // r[n] = sig[160 fr + n] * w[n]; lane l loads z[l + 16 m2] = (r[2l+32m2], r[2l+32m2+1]).
+    const float* sp = sig + fr * kHop + 2 * l;
+    cf a[16];
+#pragma unroll
+    for (int m2 = 0; m2 < 12; ++m2) {
+      float2 s = *reinterpret_cast<const float2*>(sp + 32 * m2);
+      a[m2] = {s.x * wv[m2].x, s.y * wv[m2].y};
+    }
+    {
+      float2 s = make_float2(0.0f, 0.0f);
+      if (l < 8) s = *reinterpret_cast<const float2*>(sp + 384);
+      a[12] = {s.x * wv[12].x, s.y * wv[12].y};
+    }
+    a[13] = a[14] = a[15] = {0.0f, 0.0f};
+    dft16<true>(a);
+#pragma unroll
+    for (int k1 = 1; k1 < 16; ++k1) a[k1] = cmul(a[k1], t256[k1]);
+    // transpose: row k1, column l
+#pragma unroll
+    for (int k1 = 0; k1 < 16; ++k1) X[k1 * kXStride + l] = a[k1];
+    wave_lds_sync();
+#pragma unroll
+    for (int m1 = 0; m1 < 16; ++m1) a[m1] = X[l * kXStride + m1];
+    dft16<false>(a);  // a[k2] = Z[l + 16 k2]
+
+    // Split partner Z[256 - k] for k = l + 16 k2 lives in lane 16 - l,
+    // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).
+    cf b[9];
+#pragma unroll
+    for (int k2 = 0; k2 < 9; ++k2) {
+      cf src = a[(15 - k2) & 15];
+      cf sh = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
+      cf own = a[(16 - k2) & 15];
+      b[k2] = (l == 0) ? own : sh;
+    }
+    wave_lds_sync();
+    // 2E = A + conj B, 2O = (A - conj B) / i; X[k] = E + W O, X[256-k] = conj(E - W O).
+#pragma unroll
+    for (int k2 = 0; k2 < 9; ++k2) {
+      cf A = a[k2], B = b[k2];
+      cf e = {A.x + B.x, A.y - B.y};
+      cf o = {A.y + B.y, B.x - A.x};
+      cf t = cmul(o, t512[k2]);
+      cf xp = cadd(e, t), xm = csub(e, t);
+      float pp = xp.x * xp.x + xp.y * xp.y;
+      float pm = xm.x * xm.x + xm.y * xm.y;
+      int k = l + 16 * k2;
+      if (k2 < 8) {
+        P[k] = pp;
+        P[256 - k] = pm;
+      } else if (l == 0) {
+        P[128] = pp;
+      }
+    }
+    wave_lds_sync();
+    // mel contraction over each filter's contiguous band, then the guarded log
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int m = l + 16 * i;
+      int cnt = melcnt[m], base = mello[m];
+      const float* w = melw + m * kMelW;
+      float acc = 0.0f;
+      for (int c = 0; c < cnt; ++c) acc = fmaf(w[c], P[base + c], acc);
+      float v = acc + kGuard;
+      lm[m * kLmStride + fr] = (v == kGuard) ? kLnGuard : __log2f(v) * kLn2;
+    }
+    wave_lds_sync();
+  }
+  __syncthreads();
+
+  float* o = out + it.out_off;
+  const int T = it.T;
+  for (int j = tid; j < kMel * kTile; j += kThreads) {
+    int m = j / kTile, t = j % kTile;
+    if (t < nf) o[(int64_t)m * T + f0 + t] = lm[m * kLmStride + t];
+  }
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                                            // round to nearest even
+  return (uint16_t)(u >> 16);
+}
+
+// One wavefront per (item, feature) row.  Statistics are exact (f64) for
+// ordinary rows.  A row whose values are all bitwise equal is where the
+// reference's sequential f32 sums decide the result (their rounding leaves
+// x - mean != 0, e.g. about +-0.93 for digital silence); lane 0 replays
+// those sums in the reference's order so such rows match it bit for bit.
+__global__ __launch_bounds__(kThreads) void sfe_norm_kernel(const float* __restrict__ raw,
+                                                            const Item* __restrict__ items, int n_items,
+                                                            float* __restrict__ out_f32,
+                                                            uint16_t* __restrict__ out_bf16) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= (int64_t)n_items * kMel) return;
+  const Item it = items[row / kMel];
+  const int m = (int)(row % kMel);
+  const int T = it.T;
+  const int64_t off = it.out_off + (int64_t)m * T;
+  const float* x = raw + off;
+
+  const float x0 = x[0];
+  double s = 0.0;
+  bool eq = true;
+  for (int t = lane; t < T; t += 64) {
+    float v = x[t];
+    s += (double)v;
+    eq = eq && (v == x0);
+  }
+  const bool constant = __all(eq);
+  float meanf, sdf;
+  if (constant) {
+    float r0 = 0.0f, r1 = 0.0f;
+    if (lane == 0) {
+      float sum = 0.0f;
+      for (int t = 0; t < T; ++t) sum = __fadd_rn(sum, x0);
+      float mean = __fdiv_rn(sum, (float)T);
+      float d = __fsub_rn(x0, mean);
+      float acc = 0.0f;
+      for (int t = 0; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(d, d));
+      float var = __fdiv_rn(acc, __fsub_rn((float)T, 1.0f));
+      r0 = mean;
+      r1 = __fadd_rn(__fsqrt_rn(var), 1e-5f);
+    }
+    meanf = __shfl(r0, 0, 64);
+    sdf = __shfl(r1, 0, 64);
+  } else {
+    s = wave_sum(s);
+    const double mean = s / (double)T;
+    double q = 0.0;
+    for (int t = lane; t < T; t += 64) {
+      double d = (double)x[t] - mean;
+      q += d * d;
+    }
+    q = wave_sum(q);
+    const double var = q / (double)(T - 1);  // T == 1 gives NaN, as the reference
+    meanf = (float)mean;
+    sdf = __fadd_rn(__fsqrt_rn((float)var), 1e-5f);
+  }
+  for (int t = lane; t < T; t += 64) {
+    float y = __fdiv_rn(__fsub_rn(x[t], meanf), sdf);
+    if (out_bf16) out_bf16[off + t] = f32_to_bf16(y);
+    else out_f32[off + t] = y;
+  }
+}
+
+}  // namespace
+
+int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
+
+hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int total_tiles,
+                         const DevTables* tables, float preemph, float* raw_out, hipStream_t stream) {
+  if (total_tiles <= 0) return hipSuccess;
+  sfe_logmel_kernel<<<dim3(total_tiles), dim3(kThreads), 0, stream>>>(samples, items, n_items, tables, preemph,
+                                                                       raw_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm(const float* raw, const Item* items, int n_items, void* out, bool out_bf16,
+                       hipStream_t stream) {
+  const int64_t rows = (int64_t)n_items * kMel;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks <= 0) return hipSuccess;
+  sfe_norm_kernel<<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
+      raw, items, n_items, out_bf16 ? nullptr : static_cast<float*>(out),
+      out_bf16 ? static_cast<uint16_t*>(out) : nullptr);
+  return hipGetLastError();
+}
+
+}  // namespace sfe

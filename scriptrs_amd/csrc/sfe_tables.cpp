@@ -1,0 +1,100 @@
+// Host-side construction of the constant tables the kernels read.
+//
+// hann_window and mel_filterbank follow src/frontend.rs:161-223 with the
+// reference's operation order and precision (f32 for the window, f64 for
+// the mel points and triangle weights with an f32 cast, then an f32
+// multiply by the f32-cast Slaney norm).  This file is built with
+// -ffp-contract=off so each operation rounds as in the reference.
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "sfe_internal.hpp"
+
+namespace sfe {
+
+void hann_window(int win, float* out) {
+  const float pi = 3.14159265358979323846f;  // std::f32::consts::PI
+  for (int n = 0; n < win; ++n) {
+    float num = (2.0f * pi) * (float)n;
+    float den = (float)win - 1.0f;
+    out[n] = 0.5f - 0.5f * cosf(num / den);
+  }
+}
+
+namespace {
+const double kFsp = 200.0 / 3.0;            // F_SP, src/frontend.rs:167
+const double kMinLogHz = 1000.0;            // MIN_LOG_HZ
+const double kLogStep = 0.06875177742094912;  // LOG_STEP = ln(6.4)/27
+
+double hz_to_mel(double hz) {
+  const double min_log_mel = kMinLogHz / kFsp;
+  return hz < kMinLogHz ? hz / kFsp : min_log_mel + log(hz / kMinLogHz) / kLogStep;
+}
+
+double mel_to_hz(double mel) {
+  const double min_log_mel = kMinLogHz / kFsp;
+  return mel < min_log_mel ? mel * kFsp : kMinLogHz * exp((mel - min_log_mel) * kLogStep);
+}
+}  // namespace
+
+void mel_filterbank(int n_fft, int n_mels, int sample_rate, float* out) {
+  const int bins = n_fft / 2 + 1;
+  const double mel_min = hz_to_mel(0.0);
+  const double mel_max = hz_to_mel((double)sample_rate / 2.0);
+  std::vector<double> pts(n_mels + 2), freqs(bins), diffs(n_mels + 1);
+  for (int i = 0; i <= n_mels + 1; ++i)
+    pts[i] = mel_to_hz(mel_min + (mel_max - mel_min) * (double)i / (double)(n_mels + 1));
+  for (int k = 0; k < bins; ++k) freqs[k] = (double)k * (double)sample_rate / (double)n_fft;
+  for (int i = 0; i <= n_mels; ++i) diffs[i] = pts[i + 1] - pts[i];
+  for (int m = 0; m < n_mels; ++m)
+    for (int k = 0; k < bins; ++k) {
+      double lower = (freqs[k] - pts[m]) / diffs[m];
+      double upper = (pts[m + 2] - freqs[k]) / diffs[m + 1];
+      double v = lower < upper ? lower : upper;
+      out[(size_t)m * bins + k] = (float)(v > 0.0 ? v : 0.0);
+    }
+  for (int m = 0; m < n_mels; ++m) {
+    float enorm = (float)(2.0 / (pts[m + 2] - pts[m]));
+    for (int k = 0; k < bins; ++k) out[(size_t)m * bins + k] *= enorm;
+  }
+}
+
+bool build_dev_tables(int sample_rate, DevTables* t) {
+  memset(t, 0, sizeof(*t));
+  hann_window(kWin, t->window);
+  for (int j = 0; j < 256; ++j) {
+    // laid out per lane so the kernel indexes it affinely (l * 16 + k1)
+    double a = -2.0 * M_PI * (double)((j / 16) * (j % 16)) / 256.0;
+    t->tw256[j] = make_float2((float)cos(a), (float)sin(a));
+    double b = -2.0 * M_PI * (double)j / 512.0;
+    t->tw512[j] = make_float2((float)cos(b), (float)sin(b));
+  }
+  std::vector<float> fb((size_t)kMel * kBins);
+  mel_filterbank(kNfft, kMel, sample_rate, fb.data());
+  for (int m = 0; m < kMel; ++m) {
+    const float* row = &fb[(size_t)m * kBins];
+    int lo = -1, hi = -1;
+    for (int k = 0; k < kBins; ++k)
+      if (row[k] != 0.0f) {
+        if (lo < 0) lo = k;
+        hi = k;
+      }
+    if (lo < 0) {  // an all-zero filter contributes nothing
+      t->mel_lo[m] = 0;
+      t->mel_cnt[m] = 0;
+      continue;
+    }
+    int cnt = hi - lo + 1;
+    if (cnt > kMelW) return false;
+    t->mel_lo[m] = lo;
+    t->mel_cnt[m] = cnt;
+    // x0.25 is exact (power of two) and undoes the 4x of the kernel's
+    // unscaled even/odd split.
+    for (int c = 0; c < cnt; ++c) t->mel_w[m * kMelW + c] = row[lo + c] * 0.25f;
+  }
+  return true;
+}
+
+}  // namespace sfe

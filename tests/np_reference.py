@@ -1,0 +1,84 @@
+"""Independent float64 numpy restatement of the log-mel front end.
+
+Written from the mathematics of src/frontend.rs:104-241 rather than from the
+C oracle: vectorised framing, ``numpy.fft.rfft`` (a library FFT) and a dense
+matmul, all in float64.  Used to pin the oracle (and the GPU path) against a
+third implementation whose rounding error is ~1e-13.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+N_FFT, WIN, HOP, N_MELS, SR = 512, 400, 160, 128, 16000
+
+
+def hann_window_f32(win: int = WIN) -> np.ndarray:
+    """The reference's window with float32 operations.  The cosine is the C
+    library's cosf, which is what Rust's f32::cos calls on Linux (glibc's
+    cosf is not correctly rounded everywhere; numpy's float32 cos differs
+    from it by an ulp at a few taps)."""
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.cosf.argtypes = [ctypes.c_float]
+    libm.cosf.restype = ctypes.c_float
+    n = np.arange(win, dtype=np.float32)
+    arg = (np.float32(2.0) * np.float32(np.pi)) * n / (np.float32(win) - np.float32(1.0))
+    c = np.array([libm.cosf(float(v)) for v in arg], np.float32)
+    return (np.float32(0.5) - np.float32(0.5) * c).astype(np.float32)
+
+
+def slaney_mel_filterbank(n_fft: int = N_FFT, n_mels: int = N_MELS, sr: int = SR) -> np.ndarray:
+    """librosa-style Slaney filterbank (norm='slaney', htk=False), float64."""
+    f_sp = 200.0 / 3.0
+    min_log_hz, logstep = 1000.0, np.log(6.4) / 27.0
+    min_log_mel = min_log_hz / f_sp
+
+    def hz2mel(f):
+        f = np.asarray(f, np.float64)
+        return np.where(f >= min_log_hz, min_log_mel + np.log(np.maximum(f, 1e-300) / min_log_hz) / logstep, f / f_sp)
+
+    def mel2hz(m):
+        m = np.asarray(m, np.float64)
+        return np.where(m >= min_log_mel, min_log_hz * np.exp(logstep * (m - min_log_mel)), f_sp * m)
+
+    fftfreqs = np.linspace(0, sr / 2, n_fft // 2 + 1)
+    mel_f = mel2hz(np.linspace(hz2mel(0.0), hz2mel(sr / 2.0), n_mels + 2))
+    fdiff = np.diff(mel_f)
+    ramps = mel_f[:, None] - fftfreqs[None, :]
+    lower = -ramps[:-2] / fdiff[:-1, None]
+    upper = ramps[2:] / fdiff[1:, None]
+    w = np.maximum(0.0, np.minimum(lower, upper))
+    return w * (2.0 / (mel_f[2:n_mels + 2] - mel_f[:n_mels]))[:, None]
+
+
+def logmel_raw(audio: np.ndarray, window=None, fb=None) -> np.ndarray:
+    """ln(mel + 2^-24), [128, T] float64, before normalisation."""
+    x = np.asarray(audio, np.float64)
+    if x.size == 0:
+        raise ValueError("EmptyAudio")
+    w = (hann_window_f32() if window is None else window).astype(np.float64)
+    fb = slaney_mel_filterbank() if fb is None else np.asarray(fb, np.float64)
+    y = np.empty_like(x)
+    y[0] = x[0]
+    y[1:] = x[1:] - np.float64(np.float32(0.97)) * x[:-1]
+    padded = np.concatenate([np.zeros(N_FFT // 2), y, np.zeros(N_FFT // 2)])
+    T = x.size // HOP + 1
+    idx = np.arange(T)[:, None] * HOP + np.arange(WIN)[None, :]
+    frames = padded[idx] * w[None, :]
+    spec = np.abs(np.fft.rfft(frames, n=N_FFT, axis=1)) ** 2      # [T, 257]
+    mel = spec @ fb.T                                             # [T, 128]
+    return np.log(mel + 2.0 ** -24).T
+
+
+def normalize(raw: np.ndarray) -> np.ndarray:
+    """Per-feature (x - mean) / (std + 1e-5), variance over T - 1."""
+    T = raw.shape[1]
+    mean = raw.mean(axis=1, keepdims=True)
+    var = ((raw - mean) ** 2).sum(axis=1, keepdims=True) / (T - 1) if T > 1 else np.full((raw.shape[0], 1), np.nan)
+    return (raw - mean) / (np.sqrt(var) + 1e-5)
+
+
+def extract(audio: np.ndarray) -> np.ndarray:
+    """Feature-major [128, T] float64 normalised log-mel."""
+    return normalize(logmel_raw(audio))

@@ -1,0 +1,147 @@
+"""C-ABI host logic without a GPU: symbols, planner, tables, error mapping."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import planner
+from scriptrs_amd import (AudioTooLong, ChunkPreparer, EmptyAudio, InvalidModelOutput, OverlapChunkConfig,
+                          ParakeetFeatureExtractor, SampleRange, TranscriptionConfig, build_fast_execution_plan,
+                          build_tables, num_frames, parallel_worker_count)
+from scriptrs_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "scriptrs_fe.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sfe_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = header_functions()
+    assert len(names) >= 16
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.EXPORTS)
+
+
+def test_config_defaults_match_reference():
+    c = _lib.SfeConfig()
+    _lib.lib().sfe_config_default(ctypes.byref(c))
+    py = TranscriptionConfig()
+    assert (c.sample_rate, c.feature_size, c.n_fft, c.win_length, c.hop_length, c.max_audio_samples,
+            c.samples_per_encoder_frame) == (16000, 128, 512, 400, 160, 240000, 1280)
+    assert abs(c.preemphasis - 0.97) < 1e-7
+    assert py.max_feature_frames() == 1501 and py.max_duration_seconds() == 15.0
+    o = _lib.SfeOverlapConfig()
+    _lib.lib().sfe_overlap_config_default(ctypes.byref(o))
+    assert (o.overlap_seconds, o.context_samples, o.max_model_samples) == (2.0, 1280, 240000)
+
+
+@pytest.mark.parametrize("n", [1, 159, 160, 161, 16000, 240000, 57_600_000])
+def test_num_frames(n):
+    assert num_frames(n) == n // 160 + 1 == oracle.num_frames(n)
+
+
+def test_tables_bit_exact_with_oracle():
+    w, fb = build_tables()
+    assert np.array_equal(w, oracle.hann_window())
+    assert np.array_equal(fb, oracle.mel_filterbank())
+    w2, fb2 = build_tables(TranscriptionConfig(sample_rate=22050))
+    assert np.array_equal(fb2, oracle.mel_filterbank(512, 128, 22050))
+
+
+LENGTHS = [0, 1, 1279, 1280, 95_999, 96_000, 238_079, 238_080, 238_081, 240_000, 240_001, 444_160,
+           444_161, 650_240, 1_000_003, 57_600_000, 460_800_000]
+
+
+@pytest.mark.parametrize("n", LENGTHS)
+def test_library_planner_matches_oracle_planner(n):
+    got = build_fast_execution_plan(n)
+    want = planner.build_fast_execution_plan(n)
+    assert [(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples) for t in got] == \
+        [(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples) for t in want]
+
+
+@pytest.mark.parametrize("cfg", [(2.0, 1280, 240000), (0.5, 0, 100000), (30.0, 1280, 240000), (1.0, 5000, 48000),
+                                 (0.0, 1280, 2000), (-1.0, 1280, 240000)])
+def test_planner_configs(cfg):
+    c = OverlapChunkConfig(*cfg)
+    o = planner.OverlapChunkConfig(*cfg)
+    for n in (0, 1, 5000, 123_457, 2_000_000):
+        got = c.tasks(n)
+        want = [t for t in _oracle_tasks(o, n)]
+        assert [(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples) for t in got] == want
+
+
+def _oracle_tasks(o, n):
+    out = []
+    for s, e in o.plan(0, n):
+        cs = max(s - o.context_samples, 0)
+        out.append((cs, e, s, s - cs))
+    return out
+
+
+def test_plan_sample_range():
+    got = OverlapChunkConfig().plan(SampleRange(0, 600_000))
+    assert len(got) > 1 and got[1].start < got[0].end  # src/long_form/planner.rs:376-385
+
+
+def test_worker_count():
+    assert [parallel_worker_count(*a) for a in [(0, 4), (1, 4), (3, 0), (3, 2), (3, 8)]] == [1, 1, 1, 2, 3]
+
+
+def test_plan_buffer_too_small_reports_count():
+    c = OverlapChunkConfig()._c()
+    n = ctypes.c_int32(0)
+    arr = (_lib.SfeChunk * 2)()
+    rc = _lib.lib().sfe_plan_fast(ctypes.byref(c), 57_600_000, arr, 2, ctypes.byref(n))
+    assert rc == _lib.SFE_INVALID_ARG and n.value == 280
+    assert arr[0].audio_end == 238_080 and arr[1].audio_start == 206_080 - 1280
+    assert "too small" in _lib.last_error()
+
+
+# ---- errors map onto the reference's TranscriptionError without touching a GPU ----
+
+def test_empty_audio():
+    with pytest.raises(EmptyAudio):
+        ParakeetFeatureExtractor().extract(np.zeros(0, np.float32))
+    with pytest.raises(EmptyAudio):
+        ChunkPreparer().prepare([])
+
+
+def test_audio_too_long():
+    with pytest.raises(AudioTooLong) as e:
+        ChunkPreparer().prepare(np.zeros(240_001, np.float32))
+    assert e.value.max_seconds == 15.0 and abs(e.value.actual_seconds - 15.0000625) < 1e-9
+    assert "actual=15.00s max=15.00s" in str(e.value)
+
+
+def test_c_abi_argument_errors():
+    L = _lib.lib()
+    assert L.sfe_extract(None, None, 0, None, 0) == _lib.SFE_EMPTY_AUDIO
+    assert L.sfe_extract(None, (ctypes.c_float * 4)(), 4, (ctypes.c_float * 512)(), 512) == _lib.SFE_INVALID_ARG
+    assert "null context" in _lib.last_error()
+    fo = (ctypes.c_int64 * 3)()
+    off = (ctypes.c_int64 * 3)(0, 10, 5)
+    assert L.sfe_extract_batch(None, ctypes.c_void_p(16), off, 2, 0, ctypes.c_void_p(16), fo, None) == \
+        _lib.SFE_INVALID_ARG
+    assert "non-decreasing" in _lib.last_error()
+    bad = _lib.SfeConfig()
+    L.sfe_config_default(ctypes.byref(bad))
+    bad.n_fft = 1024
+    ctx = ctypes.c_void_p()
+    assert L.sfe_create(ctypes.byref(bad), 0, ctypes.byref(ctx)) == _lib.SFE_INVALID_ARG
+    assert "specialised" in _lib.last_error()
+
+
+def test_unsupported_dtype_rejected_before_device():
+    with pytest.raises(InvalidModelOutput):
+        from scriptrs_amd.frontend import _dtype_code
+        _dtype_code("f16")

@@ -1,0 +1,118 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle."""
+import numpy as np
+import pytest
+
+import oracle
+import np_reference as R
+from conftest import assert_parity
+from scriptrs_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+def test_config1_clip(extractor):
+    _flush("case: config-1 10 s clip seed 1")
+    a = synth.sinusoids(160_000, 1)
+    got = extractor.extract(a)
+    want = oracle.extract(a).T
+    assert got.shape == (1001, 128)
+    err, widened = assert_parity(got, want, R.extract(a).T, what="config1")
+    print("max abs err", err, "widened", widened)
+
+
+@pytest.mark.parametrize("n", [1, 2, 159, 160, 161, 319, 320, 400, 401, 511, 512, 513, 5119, 5120, 5121,
+                               16_000, 48_123, 240_000])
+def test_lengths(extractor, n):
+    _flush(f"case: length {n}")
+    a = synth.sinusoids(n, 100 + n)
+    got = extractor.extract(a)
+    want = oracle.extract(a).T
+    assert got.shape == (n // 160 + 1, 128)
+    assert_parity(got, want, R.extract(a).T, what=f"len {n}")
+
+
+def test_zero_audio_matches_reference_rounding(extractor):
+    """Digital silence: every row is constant ln(2^-24); the reference's
+    sequential f32 mean leaves x - mean != 0, so the output is a constant
+    that the GPU must reproduce bit for bit."""
+    _flush("case: zero audio")
+    for n in (16_000, 160_000, 240_000):
+        a = np.zeros(n, np.float32)
+        got = extractor.extract(a)
+        want = oracle.extract(a).T
+        assert np.array_equal(got, want), n
+
+
+def test_dense_batch(extractor):
+    import torch
+    _flush("case: dense batch 8 x 240000")
+    x = synth.dense_batch(8, 240_000, 7)
+    dev = torch.from_numpy(x.reshape(-1)).cuda()
+    off = np.arange(9, dtype=np.int64) * 240_000
+    out, fo = extractor.extract_batch(dev, off)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    assert list(np.diff(fo)) == [1501] * 8
+    for i in range(8):
+        want = oracle.extract(x[i])
+        assert_parity(out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1), want, R.extract(x[i]), what=f"clip {i}")
+
+
+def test_ragged_batch(extractor):
+    import torch
+    _flush("case: ragged batch 24")
+    flat, off = synth.ragged_batch(24, 11)
+    dev = torch.from_numpy(flat).cuda()
+    out, fo = extractor.extract_batch(dev, off)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    want, wfo = oracle.extract_spans(flat, off[:-1], np.diff(off))
+    assert np.array_equal(fo, wfo)
+    ref = np.concatenate([R.extract(flat[off[i]:off[i + 1]]).reshape(-1) for i in range(24)])
+    assert_parity(out, want, ref, what="ragged")
+
+
+def test_long_form_chunks(extractor):
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: long form 1.5M samples")
+    rec = synth.speech_like(1_500_000, 5)
+    tasks = build_fast_execution_plan(rec.size)
+    dev = torch.from_numpy(rec).cuda()
+    out, fo = extractor.extract_chunks(dev, tasks)
+    torch.cuda.synchronize()
+    starts = [t.audio_start for t in tasks]
+    lens = [t.audio_end - t.audio_start for t in tasks]
+    want, wfo = oracle.extract_spans(rec, starts, lens)
+    assert np.array_equal(fo, wfo)
+    ref = np.concatenate([R.extract(rec[s:s + n]).reshape(-1) for s, n in zip(starts, lens)])
+    err, widened = assert_parity(out.cpu().numpy(), want, ref, what="long form")
+    print("max abs err", err, "widened", widened)
+
+
+def test_bf16_matches_rounded_f32(extractor):
+    import torch
+    _flush("case: bf16 output")
+    flat, off = synth.ragged_batch(6, 3)
+    dev = torch.from_numpy(flat).cuda()
+    o32, _ = extractor.extract_batch(dev, off, dtype="f32")
+    o16, _ = extractor.extract_batch(dev, off, dtype="bf16")
+    torch.cuda.synchronize()
+    assert torch.equal(o32.to(torch.bfloat16), o16)
+
+
+def test_streamed_equals_resident(extractor):
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: streamed 3M samples")
+    rec = synth.speech_like(3_000_000, 9)
+    tasks = build_fast_execution_plan(rec.size)
+    a, fa = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+    b, fb = extractor.extract_chunks_streamed(rec, tasks, window_samples=960_000)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)

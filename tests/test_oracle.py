@@ -1,0 +1,233 @@
+"""Pins the CPU oracle (oracle/sfe_oracle.c, oracle/planner.py) without a GPU.
+
+Each check is chosen so that a plausible restatement mistake fails it:
+window off by one (N vs N-1), centred instead of left-aligned frames, wrong
+padding, missing preemphasis or a preemphasis that does not restart,
+variance over T instead of T-1, epsilon on the variance instead of the std,
+a wrong guard, or a transposed filterbank.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import np_reference as R
+import oracle
+from oracle import planner
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def sine(freq, n, sr=16000):
+    t = np.arange(n, dtype=np.float32)
+    return np.sin(np.float32(2 * np.pi) * np.float32(freq) * t / np.float32(sr)).astype(np.float32)
+
+
+# ---- tables -------------------------------------------------------------------
+
+def test_hann_window_bit_exact_and_symmetric():
+    w = oracle.hann_window()
+    assert w.dtype == np.float32 and w.shape == (400,)
+    assert np.array_equal(w, R.hann_window_f32())     # same f32 expression, evaluated by numpy
+    assert w[0] == 0.0 and w[-1] < 1e-6               # symmetric Hann: (N-1) denominator
+    np.testing.assert_allclose(w, w[::-1], atol=5e-7)
+    # periodic Hann (N denominator) would differ by ~4e-5 at the ends
+    periodic = 0.5 - 0.5 * np.cos(2 * np.pi * np.arange(400) / 400)
+    assert np.abs(w - periodic).max() > 1e-3
+
+
+def test_filterbank_matches_slaney_definition():
+    fb = oracle.mel_filterbank()
+    ref = R.slaney_mel_filterbank()
+    assert fb.shape == (128, 257)
+    np.testing.assert_allclose(fb, ref, rtol=2e-6, atol=1e-9)
+    assert int((fb != 0).sum()) == 504
+    assert (fb != 0).sum(1).max() == 12 and (fb != 0).sum(0).max() == 2
+    assert np.all((fb != 0).sum(1) > 0)                # no empty filter
+    # triangles: contiguous support, centres strictly increasing (not transposed)
+    lo = [np.nonzero(r)[0].min() for r in fb]
+    hi = [np.nonzero(r)[0].max() for r in fb]
+    assert all(int((fb[m] != 0).sum()) == hi[m] - lo[m] + 1 for m in range(128))
+    centres = (fb * np.arange(257)).sum(1) / fb.sum(1)
+    assert np.all(np.diff(centres) > 0)
+
+
+# ---- reference tests (src/frontend.rs:258-300) ------------------------------------
+
+def test_stft_concentrates_power_at_the_expected_bin():
+    spec = oracle.stft_power(sine(1000.0, 16000))
+    peaks = spec[:, 2:spec.shape[1] - 2].argmax(0)
+    assert (peaks == 32).sum() > 90
+
+
+def test_feature_extraction_produces_expected_shape():
+    f = oracle.extract(sine(440.0, 16000)).T
+    assert f.shape[1] == 128 and f.shape[0] > 0 and f.shape[0] == 101
+
+
+def test_features_are_column_normalized():
+    f = oracle.extract(sine(440.0, 16000)).T
+    assert abs(f[:, 0].mean()) < 1e-4
+
+
+# ---- closed forms and brute force ---------------------------------------------------
+
+def test_stft_power_matches_brute_force_dft():
+    rng = np.random.default_rng(0)
+    a = (0.3 * rng.standard_normal(700)).astype(np.float32)
+    p = oracle.stft_power(a)
+    # brute-force DFT of the left-aligned, zero-padded, preemphasised frames
+    y = np.concatenate([[a[0]], a[1:].astype(np.float64) - np.float64(np.float32(0.97)) * a[:-1]])
+    pad = np.concatenate([np.zeros(256), y, np.zeros(256)])
+    w = oracle.hann_window().astype(np.float64)
+    k = np.arange(257)[:, None] * np.arange(512)[None, :]
+    M = np.exp(-2j * np.pi * k / 512)
+    for f in range(p.shape[1]):
+        r = np.zeros(512)
+        r[:400] = pad[160 * f:160 * f + 400] * w
+        want = np.abs(M @ r) ** 2
+        np.testing.assert_allclose(p[:, f], want, rtol=2e-4, atol=2e-5 * want.max())
+
+
+def test_impulse_power_is_window_tap_squared():
+    """A unit impulse at sample s (with its preemphasis echo -0.97 at s+1)
+    gives |w[n] - 0.97 w[n+1]|^2-shaped spectra; a frame seeing only the
+    first tap at offset n has flat power w[n]^2."""
+    a = np.zeros(1000, np.float32)
+    a[999] = 1.0                       # echo falls outside the signal
+    p = oracle.stft_power(a)
+    w = oracle.hann_window()
+    # frame f sees sample 999 at window offset 999 + 256 - 160 f
+    for f in range(p.shape[1]):
+        n = 999 + 256 - 160 * f
+        want = w[n] ** 2 if 0 <= n < 400 else 0.0
+        np.testing.assert_allclose(p[:, f], np.full(257, want), rtol=1e-6, atol=1e-12)
+
+
+def test_parseval_per_frame():
+    rng = np.random.default_rng(1)
+    a = (0.2 * rng.standard_normal(3000)).astype(np.float32)
+    p = oracle.stft_power(a).astype(np.float64)
+    y = np.concatenate([[a[0]], a[1:].astype(np.float64) - 0.97 * a[:-1]])
+    pad = np.concatenate([np.zeros(256), y, np.zeros(256)])
+    w = oracle.hann_window().astype(np.float64)
+    for f in range(p.shape[1]):
+        e = ((pad[160 * f:160 * f + 400] * w) ** 2).sum()
+        tot = p[0, f] + p[256, f] + 2 * p[1:256, f].sum()
+        assert abs(tot - 512 * e) <= 1e-4 * 512 * e + 1e-9
+
+
+def test_zero_audio_reproduces_sequential_f32_rounding():
+    """Every row is constant ln(2^-24).  The reference's sequential f32 mean
+    is not exactly that constant, so the output is (x-mean)/(|x-mean|+1e-5),
+    about +-0.93, replayed here with numpy float32 scalars."""
+    for n in (1600, 16_000, 160_000):
+        out = oracle.extract(np.zeros(n, np.float32))
+        T = n // 160 + 1
+        x = np.float32(np.log(np.float32(2.0 ** -24)))
+        s = np.float32(0)
+        for _ in range(T):
+            s = np.float32(s + x)
+        mean = np.float32(s / np.float32(T))
+        d = np.float32(x - mean)
+        v = np.float32(0)
+        for _ in range(T):
+            v = np.float32(v + np.float32(d * d))
+        sd = np.float32(np.sqrt(np.float32(v / np.float32(T - 1))) + np.float32(1e-5))
+        assert np.all(out == np.float32(d / sd)), n
+    assert abs(oracle.extract(np.zeros(160_000, np.float32))[0, 0] - 0.93169063) < 1e-7
+
+
+def test_single_frame_is_nan_like_reference():
+    # T = 1: variance divides by T - 1 = 0 (src/frontend.rs:235)
+    out = oracle.extract(np.full(100, 0.1, np.float32))
+    assert out.shape == (128, 1) and np.all(np.isnan(out))
+
+
+def test_preemphasis_restarts_per_span():
+    a = (0.1 * np.random.default_rng(2).standard_normal(40_000)).astype(np.float32)
+    out, fo = oracle.extract_spans(a, [0, 15_000], [20_000, 25_000], nthreads=2)
+    np.testing.assert_array_equal(out[:128 * fo[1]], oracle.extract(a[:20_000]).reshape(-1))
+    np.testing.assert_array_equal(out[128 * fo[1]:], oracle.extract(a[15_000:]).reshape(-1))
+
+
+@pytest.mark.parametrize("name", ["sine1k_1s", "sine440_1s", "impulse_4000", "chirp_7777", "noise_5000"])
+def test_oracle_against_float64_fixtures(name):
+    g = np.load(os.path.join(GOLDEN, "logmel_small.npz"))
+    a = g[name + "_audio"]
+    raw64 = g[name + "_logmel_raw64"].astype(np.float64)
+    feat64 = g[name + "_features64"].astype(np.float64)
+    # fixtures still match the float64 restatement they were made from
+    np.testing.assert_allclose(R.logmel_raw(a), raw64, rtol=1e-6, atol=1e-5)
+    out = oracle.extract(a)
+    assert out.shape == feat64.shape
+    # f32 rounding of the raw log-mel: tight except where mel ~ guard
+    mel64 = np.exp(raw64) - 2.0 ** -24
+    strong = mel64 > 1e-3
+    raw32 = np.log(np.exp(raw64))  # identity, keeps shapes explicit
+    assert strong.any()
+    err = np.abs(out - feat64)
+    std = np.sqrt(((raw64 - raw64.mean(1, keepdims=True)) ** 2).sum(1, keepdims=True) / (raw64.shape[1] - 1))
+    # normalised error = raw error / std; raw f32 log error is ~1e-6 on strong bins
+    assert np.all(err[np.broadcast_to(strong, err.shape)] <= 1e-4 + 1e-3 * np.abs(feat64[strong]) + 1e-5 / std.min())
+    assert np.nanmax(err) < 5e-3
+    del raw32
+
+
+def test_centred_frames_would_fail():
+    """Guard against a torch-style centred window: shifting frames by 56
+    samples changes the features far beyond tolerance."""
+    a = sine(440.0, 16000) * np.float32(0.5)
+    out = oracle.extract(a)
+    shifted = R.extract(np.concatenate([np.zeros(56, np.float32), a])[:16000])
+    assert np.abs(out - shifted).max() > 1e-2
+
+
+# ---- planner ------------------------------------------------------------------------
+
+def test_planner_constants():
+    c = planner.OverlapChunkConfig()
+    assert (c.chunk_samples(), c.overlap_samples(), c.stride_samples()) == (238_080, 32_000, 206_080)
+
+
+def test_overlap_plan_advances_with_stride():
+    # src/long_form/planner.rs:376-385
+    chunks = planner.OverlapChunkConfig().plan(0, 600_000)
+    assert len(chunks) > 1 and chunks[1][0] < chunks[0][1]
+
+
+def test_fast_plan_context_and_order():
+    # src/long_form.rs:724-735 invariants on the fast plan
+    for n in (96_000, 600_000, 5_000_000):
+        t = planner.build_fast_execution_plan(n)
+        assert t and t[-1].audio_end == n
+        assert all(a.global_sample_offset <= b.global_sample_offset for a, b in zip(t, t[1:]))
+        assert all(x.context_samples <= x.global_sample_offset for x in t)
+        assert all(x.audio_end - x.audio_start <= 240_000 for x in t)
+
+
+def test_parallel_worker_count():
+    # src/long_form.rs:738-745
+    assert planner.parallel_worker_count(0, 4) == 1
+    assert planner.parallel_worker_count(1, 4) == 1
+    assert planner.parallel_worker_count(3, 0) == 1
+    assert planner.parallel_worker_count(3, 2) == 2
+    assert planner.parallel_worker_count(3, 8) == 3
+
+
+def test_planner_fixtures():
+    with open(os.path.join(GOLDEN, "planner_tables.json")) as f:
+        tables = json.load(f)
+    for tab in tables:
+        t = planner.build_fast_execution_plan(tab["audio_len"])
+        assert len(t) == tab["count"]
+        if t:
+            assert [t[0].audio_start, t[0].audio_end, t[0].global_sample_offset, t[0].context_samples] == tab["first"]
+            assert [t[-1].audio_start, t[-1].audio_end, t[-1].global_sample_offset, t[-1].context_samples] == tab["last"]
+        assert sum(x.audio_end - x.audio_start for x in t) == tab["sum_len"]
+        assert sum((x.audio_end - x.audio_start) // 160 + 1 for x in t) == tab["sum_frames"]
+    by_len = {t["audio_len"]: t for t in tables}
+    # the benchmark chunk tables
+    assert (by_len[57_600_000]["count"], by_len[57_600_000]["sum_frames"]) == (280, 418_312)
+    assert (by_len[460_800_000]["count"], by_len[460_800_000]["sum_frames"]) == (2236, 3_347_116)
