@@ -48,6 +48,14 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is not None:
         return _lib
+    # torch ships its own libamdhip64 with the same soname (libamdhip64.so.7).
+    # Whichever is loaded first serves the whole process, so load torch's
+    # first: then this library and torch share one HIP runtime, and device
+    # pointers and streams pass freely between them.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(
             f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "

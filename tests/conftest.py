@@ -31,30 +31,32 @@ def assert_close(got, want, atol=ATOL, rtol=RTOL, what=""):
     return float(err.max()) if err.size else 0.0
 
 
-def assert_parity(got, oracle_out, ref64, atol=ATOL, rtol=RTOL, what=""):
-    """GPU vs oracle at the north-star bar, widened only by the oracle's own f32 noise.
+def assert_parity(got, oracle_out, ref64, env, atol=ATOL, rtol=RTOL, what=""):
+    """GPU vs oracle at the north-star bar, widened only by the f32 noise envelope.
 
-    Both the oracle and the reference compute in f32.  Where a mel bin's
-    energy sits near the 2^-24 guard, their f32 FFT rounding noise moves the
-    normalised value by up to ~1e-3, so no f32 implementation can agree with
-    another to 1e-4 there.  The float64 numpy restatement ``ref64``
-    measures that noise per element: ``noise = |oracle - ref64|``.  Checks:
-      |got - oracle| <= atol + rtol*|oracle| + 2*noise
-      |got - ref64|  <= atol + rtol*|ref64|  + 2*noise
-    (GPU no farther from exact than the oracle's own f32 computation).
-    Returns (max |got-oracle|, number of elements whose bound was widened)."""
+    The oracle and the reference both compute in f32.  Where a mel bin's
+    energy sits near the 2^-24 guard, f32 FFT rounding moves the normalised
+    value by up to ~1e-3, so no two f32 implementations agree to 1e-4 there.
+    ``env`` (tests/np_reference.py:f32_noise_envelope) is the analytic scale
+    of that noise per element.  Checks, per element:
+      |got - ref64| <= atol + rtol*|ref64| + env         (GPU within f32 noise of exact)
+    and either
+      |got - oracle| <= atol + rtol*|oracle| + 2*env     (two f32 implementations agree)
+    or |got - ref64| <= |oracle - ref64|                 (GPU closer to exact than the
+                                                          oracle's radix-2 f32 FFT)
+    Returns (max |got-oracle|, number of elements that needed the widening)."""
     import numpy as np
     g = np.asarray(got, np.float64)
     o = np.asarray(oracle_out, np.float64)
     r = np.asarray(ref64, np.float64)
-    assert g.shape == o.shape == r.shape, (g.shape, o.shape, r.shape)
+    n = np.asarray(env, np.float64)
+    assert g.shape == o.shape == r.shape == n.shape, (g.shape, o.shape, r.shape, n.shape)
     nan = np.isnan(o)
     assert np.array_equal(np.isnan(g), nan), f"{what}: NaN pattern differs"
-    g, o, r = g[~nan], o[~nan], r[~nan]
-    noise = np.abs(o - r)
+    g, o, r, n = g[~nan], o[~nan], r[~nan], n[~nan]
     base = atol + rtol * np.abs(o)
-    b1 = np.abs(g - o) > base + 2 * noise
-    b2 = np.abs(g - r) > atol + rtol * np.abs(r) + 2 * noise
+    b1 = (np.abs(g - o) > base + 2 * n) & (np.abs(g - r) > np.abs(o - r))
+    b2 = np.abs(g - r) > atol + rtol * np.abs(r) + n
     assert not b1.any(), f"{what}: {b1.sum()} of {b1.size} outside oracle bound, max {np.abs(g - o).max():.3e}"
     assert not b2.any(), f"{what}: {b2.sum()} of {b2.size} outside f64 bound, max {np.abs(g - r).max():.3e}"
     widened = int((np.abs(g - o) > base).sum())

@@ -82,3 +82,34 @@ def normalize(raw: np.ndarray) -> np.ndarray:
 def extract(audio: np.ndarray) -> np.ndarray:
     """Feature-major [128, T] float64 normalised log-mel."""
     return normalize(logmel_raw(audio))
+
+
+def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
+    """Per-element scale of the rounding noise any f32 FFT-based implementation
+    of the front end carries, in normalised units, [128, T].
+
+    A radix-2/4 f32 FFT of a frame r has per-bin absolute error of order
+    u * log2(N) * ||r||_2 (u = 2^-24), independent of the bin.  That moves
+    |X_k|^2 by about 2|X_k| dX + dX^2, the mel value by the filter-weighted
+    sum of that, the log by dmel / (mel + 2^-24), and the normalised output
+    by that divided by the row's std.  A floor of 4u*|raw| covers the f32 log
+    and elementwise rounding."""
+    x = np.asarray(audio, np.float64)
+    w = hann_window_f32().astype(np.float64)
+    fb = slaney_mel_filterbank()
+    y = np.empty_like(x)
+    y[0] = x[0]
+    y[1:] = x[1:] - np.float64(np.float32(0.97)) * x[:-1]
+    padded = np.concatenate([np.zeros(N_FFT // 2), y, np.zeros(N_FFT // 2)])
+    T = x.size // HOP + 1
+    idx = np.arange(T)[:, None] * HOP + np.arange(WIN)[None, :]
+    frames = padded[idx] * w[None, :]
+    X = np.abs(np.fft.rfft(frames, n=N_FFT, axis=1))
+    u = 2.0 ** -24
+    dX = u * np.log2(N_FFT) * np.sqrt((frames ** 2).sum(1, keepdims=True))
+    dP = 2.0 * X * dX + dX ** 2
+    mel = (X ** 2) @ fb.T
+    raw = np.log(mel + 2.0 ** -24)
+    d_raw = (dP @ fb.T) / (mel + 2.0 ** -24) + 4 * u * np.abs(raw)
+    std = raw.std(axis=0, ddof=1, keepdims=True) if T > 1 else np.ones((1, raw.shape[1]))
+    return (d_raw / std).T

@@ -20,7 +20,7 @@ def test_config1_clip(extractor):
     got = extractor.extract(a)
     want = oracle.extract(a).T
     assert got.shape == (1001, 128)
-    err, widened = assert_parity(got, want, R.extract(a).T, what="config1")
+    err, widened = assert_parity(got, want, R.extract(a).T, R.f32_noise_envelope(a).T, what="config1")
     print("max abs err", err, "widened", widened)
 
 
@@ -32,7 +32,7 @@ def test_lengths(extractor, n):
     got = extractor.extract(a)
     want = oracle.extract(a).T
     assert got.shape == (n // 160 + 1, 128)
-    assert_parity(got, want, R.extract(a).T, what=f"len {n}")
+    assert_parity(got, want, R.extract(a).T, R.f32_noise_envelope(a).T, what=f"len {n}")
 
 
 def test_zero_audio_matches_reference_rounding(extractor):
@@ -59,7 +59,8 @@ def test_dense_batch(extractor):
     assert list(np.diff(fo)) == [1501] * 8
     for i in range(8):
         want = oracle.extract(x[i])
-        assert_parity(out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1), want, R.extract(x[i]), what=f"clip {i}")
+        assert_parity(out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1), want, R.extract(x[i]),
+                      R.f32_noise_envelope(x[i]), what=f"clip {i}")
 
 
 def test_ragged_batch(extractor):
@@ -72,8 +73,10 @@ def test_ragged_batch(extractor):
     out = out.cpu().numpy()
     want, wfo = oracle.extract_spans(flat, off[:-1], np.diff(off))
     assert np.array_equal(fo, wfo)
-    ref = np.concatenate([R.extract(flat[off[i]:off[i + 1]]).reshape(-1) for i in range(24)])
-    assert_parity(out, want, ref, what="ragged")
+    clips = [flat[off[i]:off[i + 1]] for i in range(24)]
+    ref = np.concatenate([R.extract(c).reshape(-1) for c in clips])
+    env = np.concatenate([R.f32_noise_envelope(c).reshape(-1) for c in clips])
+    assert_parity(out, want, ref, env, what="ragged")
 
 
 def test_long_form_chunks(extractor):
@@ -90,7 +93,8 @@ def test_long_form_chunks(extractor):
     want, wfo = oracle.extract_spans(rec, starts, lens)
     assert np.array_equal(fo, wfo)
     ref = np.concatenate([R.extract(rec[s:s + n]).reshape(-1) for s, n in zip(starts, lens)])
-    err, widened = assert_parity(out.cpu().numpy(), want, ref, what="long form")
+    env = np.concatenate([R.f32_noise_envelope(rec[s:s + n]).reshape(-1) for s, n in zip(starts, lens)])
+    err, widened = assert_parity(out.cpu().numpy(), want, ref, env, what="long form")
     print("max abs err", err, "widened", widened)
 
 

@@ -231,3 +231,19 @@ def test_planner_fixtures():
     # the benchmark chunk tables
     assert (by_len[57_600_000]["count"], by_len[57_600_000]["sum_frames"]) == (280, 418_312)
     assert (by_len[460_800_000]["count"], by_len[460_800_000]["sum_frames"]) == (2236, 3_347_116)
+
+
+@pytest.mark.parametrize("kind,seed", [("sin", 1), ("sin", 2), ("speech", 3), ("speech", 8)])
+def test_f32_noise_envelope_bounds_the_oracle(kind, seed):
+    """The oracle's error against float64 stays within tol + a few envelopes
+    (its radix-2 FFT rounds more often than a radix-16 one), which validates
+    the envelope as the scale of f32 noise that the GPU parity tests allow."""
+    from scriptrs_amd import synth
+    a = synth.sinusoids(160_000, seed) if kind == "sin" else synth.speech_like(240_000, seed)[:238_080]
+    r = R.extract(a)
+    o = oracle.extract(a)
+    env = R.f32_noise_envelope(a)
+    excess = np.abs(o - r) - (1e-4 + 1e-3 * np.abs(r))
+    assert np.all(excess <= 8.0 * env)
+    # the envelope is small where the signal is strong: it is not a blanket pass
+    assert np.median(env) < 2e-5
