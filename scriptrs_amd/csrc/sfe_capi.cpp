@@ -116,6 +116,7 @@ bool shape_supported(const sfe_config* c, std::string* why) {
 struct sfe_ctx {
   sfe_config cfg;
   int device = 0;
+  int grid_cap = 512;  // resident log-mel workgroups: CUs x blocks per CU
   std::mutex mu;
   sfe::DevTables* d_tables = nullptr;
   hipStream_t s_compute = nullptr;  // internal streams, default priority
@@ -180,7 +181,7 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* d_items, int n, 
     for (int i = 0; i < 4; ++i)
       if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
   if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
-  SFE_HIP(sfe::launch_logmel(samples, d_items, n, tiles, ctx->d_tables, ctx->cfg.preemphasis, raw, stream));
+  SFE_HIP(sfe::launch_logmel(samples, d_items, n, tiles, ctx->d_tables, ctx->cfg.preemphasis, raw, ctx->grid_cap, stream));
   if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
   if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
   SFE_HIP(sfe::launch_norm(raw, d_items, n, out, out_dtype == SFE_BF16, stream));
@@ -309,6 +310,9 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
   sfe_ctx* ctx = new sfe_ctx();
   ctx->cfg = *cfg;
   ctx->device = device;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+    ctx->grid_cap = cus * sfe::kLogmelBlocksPerCU;
   auto cleanup = [&](int rc) {
     sfe_destroy(ctx);
     return rc;

@@ -13,7 +13,28 @@ constexpr int kHop = 160;
 constexpr int kMel = 128;
 constexpr int kBins = kNfft / 2 + 1;  // 257
 constexpr int kPad = kNfft / 2;       // 256 zeros each side (src/frontend.rs:124-125)
-constexpr int kMelW = 12;             // max contiguous nonzeros per filter row
+
+// Mel contraction schedule for v_mfma_f32_16x16x4_f32.  The 128 filters form
+// 8 blocks of 16; block b is contracted over kBlockSteps[b] steps of 4 bins
+// starting at a bin taken from the device table (so other sample rates work
+// when their filters fit the same step counts).  The step counts are those
+// of the 16 kHz Slaney filterbank.  Blocks are assigned to the 4 waves of a
+// workgroup at compile time so each wave's MFMA chains have static control
+// flow; the busiest wave runs 22 steps.
+constexpr int kWaves = 4;
+constexpr int kBlocks = kMel / 16;
+constexpr int kBlockSteps[kBlocks] = {4, 4, 4, 5, 8, 11, 15, 22};
+constexpr int kWaveBlocks[kWaves][3] = {{7, -1, -1}, {6, 0, -1}, {5, 3, 1}, {4, 2, -1}};
+constexpr int wave_steps(int w) {
+  int n = 0;
+  for (int i = 0; i < 3; ++i)
+    if (kWaveBlocks[w][i] >= 0) n += kBlockSteps[kWaveBlocks[w][i]];
+  return n;
+}
+constexpr int kMaxSteps = 22;  // per wave
+static_assert(wave_steps(0) <= kMaxSteps && wave_steps(1) <= kMaxSteps && wave_steps(2) <= kMaxSteps &&
+                  wave_steps(3) <= kMaxSteps,
+              "schedule exceeds the per-wave step budget");
 
 // One featurized item: a clip or a long-form chunk task.  samples[start,
 // start+len) is featurized into out[out_off + m*T + t].
@@ -30,22 +51,27 @@ struct DevTables {
   float window[kNfft];       // hann_window(400), zero past 400
   float2 tw256[256];         // [l * 16 + k1] = e^{-2 pi i l k1 / 256}, l, k1 < 16
   float2 tw512[256];         // e^{-2 pi i k / 512}, k < 256
-  int32_t mel_lo[kMel];      // first nonzero bin of filter m
-  int32_t mel_cnt[kMel];     // contiguous bins from mel_lo
-  float mel_w[kMel * kMelW]; // weights * 0.25 (the FFT stage yields 4*|X|^2)
+  int32_t block_k0[kBlocks];               // first bin of each block (multiple of 4)
+  // A operand of each step of wave w, in the wave's block order, in lane
+  // order: lane L holds W[16 b + L % 16][k0_b + 4 s + L / 16] * 0.25 (the FFT
+  // stage yields 4|X|^2)
+  float a[kWaves][kMaxSteps][64];
 };
 
 // Host table builders (sfe_tables.cpp).
 void hann_window(int win, float* out);
 void mel_filterbank(int n_fft, int n_mels, int sample_rate, float* out);
-// Returns false if some filter row has more than kMelW contiguous bins.
+// Returns false if the filterbank does not fit the MFMA schedule.
 bool build_dev_tables(int sample_rate, DevTables* t);
 
 // Kernel launchers (sfe_kernels.hip).  All asynchronous on `stream`.
-constexpr int kTile = 32;  // frames per workgroup of the log-mel kernel
+constexpr int kTile = 64;  // frames per workgroup of the log-mel kernel
 int64_t tiles_for(int64_t T);
+// grid_cap: workgroups resident on the device at once (the kernel loops
+// over tiles, so launching more than that only adds scheduling overhead).
 hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int total_tiles,
-                         const DevTables* tables, float preemph, float* raw_out, hipStream_t stream);
+                         const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream);
+constexpr int kLogmelBlocksPerCU = 2;
 // Normalises raw (f32, layout as above) per (item, feature) row and writes
 // to out (f32, may alias raw) or bf16 (uint16_t*) when out_bf16 is set.
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, void* out, bool out_bf16,

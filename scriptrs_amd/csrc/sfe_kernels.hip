@@ -27,11 +27,8 @@ namespace sfe {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kSigLen = kHop * (kTile - 1) + kWin;  // 5360 preemphasised samples per tile
 constexpr int kXStride = 17;                         // transpose row stride (complex)
 constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
-constexpr int kSlots = 16;                           // 4 waves x 4 frame groups
-constexpr int kLmStride = kTile + 1;
 constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
 // ln(2^-24) rounded to f32, the value the reference's f32 ln returns for a
 // mel value of exactly zero.
@@ -111,61 +108,86 @@ __device__ __forceinline__ void dft16(cf (&a)[16]) {
     for (int d = 0; d < 4; ++d) a[c + 4 * d] = b[4 * c + d];
 }
 
-// Orders LDS traffic between the lanes that share a frame slot.  Every wave
-// runs the same number of frame iterations, so a workgroup barrier is safe.
-__device__ __forceinline__ void wave_lds_sync() { __syncthreads(); }
+// Orders LDS traffic among the lanes of one wavefront: earlier LDS writes of
+// all lanes are visible to later reads, and the compiler keeps LDS accesses
+// on their side of it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-__global__ __launch_bounds__(kThreads) void sfe_logmel_kernel(const float* __restrict__ samples,
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Work of one workgroup: a tile of kTile frames of one item, in passes of 16
+// frames.  In a pass each of the 4 waves transforms 4 consecutive frames (16
+// lanes per frame) and writes their power spectra to the shared P buffer;
+// after one workgroup barrier every wave contracts all 16 frames with its
+// share of the mel filter blocks on the matrix cores and stores the log.
+// P is double-buffered, so the next pass's FFTs overlap this pass's MFMAs
+// and a pass needs a single barrier.
+constexpr int kPassFrames = 16;
+constexpr int kPasses = kTile / kPassFrames;
+constexpr int kSpan = 3 * kHop + kWin;  // samples under 4 consecutive frames (880)
+constexpr int kWaveBuf = 4 * kSlot * 2; // floats: 4 transpose slots; also holds the 880-sample span
+constexpr int kPStride = 258;           // floats per P row (258 = 2 mod 32: conflict-free B reads)
+static_assert(kSpan <= kWaveBuf, "span must fit the wave buffer");
+constexpr int kSpanVec = (kSpan + 255) / 256;  // 16-byte loads per lane (4)
+static_assert(kSpan % 4 == 0, "span is whole float4s");
+
+// Guarded log (src/frontend.rs:111-113): ln(v + 2^-24), with the exact
+// f32 value of ln(2^-24) when the mel value adds nothing to the guard.
+__device__ __forceinline__ float guarded_log(float v) {
+  const float u = v + kGuard;
+  return (u == kGuard) ? kLnGuard : __log2f(u) * kLn2;
+}
+
+// One filter block on the matrix cores: all B operands are read first (one
+// LDS wait), then the block's MFMA chain runs back to back.  Lane (n, kk)
+// ends with D[4 kk + r][n]: filters 16 b + 4 kk + r of frame n.
+template <int B>
+__device__ __forceinline__ void mel_block(const float* av, int k0, const float* PB, float* ot, int T, bool valid,
+                                          int kk) {
+  constexpr int S = kBlockSteps[B];
+  float bv[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) bv[s] = PB[k0 + 4 * s];
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < S; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
+  if (valid) {
+    float* row = ot + (int64_t)(16 * B + 4 * kk) * T;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) row[(int64_t)r * T] = guarded_log(acc[r]);
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void mel_wave(const float (&av)[kMaxSteps], const int (&k0b)[kBlocks], const float* PB,
+                                         float* ot, int T, bool valid, int kk) {
+  constexpr int b0 = kWaveBlocks[W][0], b1 = kWaveBlocks[W][1], b2 = kWaveBlocks[W][2];
+  mel_block<b0>(av, k0b[b0], PB, ot, T, valid, kk);
+  if constexpr (b1 >= 0) mel_block<b1>(av + kBlockSteps[b0], k0b[b1], PB, ot, T, valid, kk);
+  if constexpr (b2 >= 0) mel_block<b2>(av + kBlockSteps[b0] + kBlockSteps[b1], k0b[b2], PB, ot, T, valid, kk);
+}
+
+__global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __restrict__ samples,
                                                               const Item* __restrict__ items, int n_items,
-                                                              const DevTables* __restrict__ tb, float coef,
-                                                              float* __restrict__ out) {
-  __shared__ __align__(16) float sig[kSigLen];
-  __shared__ __align__(16) cf xch[kSlots * kSlot];
-  __shared__ __align__(16) float lm[kMel * kLmStride];
-  __shared__ __align__(16) float melw[kMel * kMelW];
-  __shared__ int mello[kMel];
-  __shared__ int melcnt[kMel];
+                                                              int total_tiles, const DevTables* __restrict__ tb,
+                                                              float coef, float* __restrict__ out) {
+  __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
+  __shared__ __align__(16) float pbuf[2][kPassFrames][kPStride];
 
   const int tid = threadIdx.x;
-  const int tile = blockIdx.x;
-  int lo = 0, hi = n_items - 1;
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (items[mid].tile_off <= tile) lo = mid;
-    else hi = mid - 1;
-  }
-  const Item it = items[lo];
-  const int f0 = (tile - it.tile_off) * kTile;
-  const int nf = min(kTile, it.T - f0);
-  const float* x = samples + it.start;
-  const int64_t L = it.len;
-  const int64_t s0 = (int64_t)f0 * kHop - kPad;
-
-  // Stage the preemphasised, zero-padded signal of the tile:
-  // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
-  // src/frontend.rs:157 computes it), zero outside [0, L).
-  for (int j = tid; j < kSigLen; j += kThreads) {
-    int64_t s = s0 + j;
-    float v = 0.0f;
-    if (s >= 0 && s < L) {
-      float cur = x[s];
-      v = (s == 0) ? cur : __fsub_rn(cur, __fmul_rn(coef, x[s - 1]));
-    }
-    sig[j] = v;
-  }
-  for (int j = tid; j < kMel * kMelW; j += kThreads) melw[j] = tb->mel_w[j];
-  if (tid < kMel) {
-    mello[tid] = tb->mel_lo[tid];
-    melcnt[tid] = tb->mel_cnt[tid];
-  }
-
   const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4;  // frame of this lane within the wave's 4
   const int l = lane & 15;
-  const int slot = (tid >> 6) * 4 + (lane >> 4);
   const int partner = (16 - l) & 15;
 
-  // Per-lane constants: window taps of this lane's inputs, inter-stage
-  // twiddles e^{-2 pi i l k1/256} and split twiddles e^{-2 pi i k/512}.
+  // Per-lane constants: window taps of this lane's FFT inputs, inter-stage
+  // twiddles e^{-2 pi i l k1/256}, split twiddles e^{-2 pi i k/512}, and the
+  // A operands (filter weights) of this wave's MFMA steps.
   cf wv[13];
 #pragma unroll
   for (int m2 = 0; m2 < 13; ++m2) {
@@ -178,38 +200,115 @@ __global__ __launch_bounds__(kThreads) void sfe_logmel_kernel(const float* __res
     // A per-lane table row, indexed affinely: hipcc 7.2 (LLVM 22) miscompiled
     // the equivalent tw[(l * k1) & 255] gather, loading .y of k1 = 1 from
     // element 2l.
-    float2 w = tb->tw256[l * 16 + k1];
-    t256[k1] = {w.x, w.y};
+    float2 tw = tb->tw256[l * 16 + k1];
+    t256[k1] = {tw.x, tw.y};
   }
   cf t512[9];
 #pragma unroll
   for (int k2 = 0; k2 < 9; ++k2) {
-    float2 w = tb->tw512[l + 16 * k2];
-    t512[k2] = {w.x, w.y};
+    float2 tw = tb->tw512[l + 16 * k2];
+    t512[k2] = {tw.x, tw.y};
   }
-  __syncthreads();
+  float av[kMaxSteps];
+#pragma unroll
+  for (int s = 0; s < kMaxSteps; ++s) av[s] = tb->a[w][s][lane];
+  int k0b[kBlocks];  // first bin of each filter block (uniform)
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b) k0b[b] = tb->block_k0[b];
 
-  cf* X = xch + slot * kSlot;
-  float* P = reinterpret_cast<float*>(X);
-  for (int fr = slot; fr < kTile; fr += kSlots) {
-    // r[n] = sig[160 fr + n] * w[n]; lane l loads z[l + 16 m2] = (r[2l+32m2], r[2l+32m2+1]).
-    const float* sp = sig + fr * kHop + 2 * l;
+  float* sb = wbuf[w];
+  cf* X = reinterpret_cast<cf*>(sb) + g * kSlot;
+  const int n = lane & 15;        // MFMA: B column (frame) / D column
+  const int kk = lane >> 4;       // MFMA: B row (bin within the step) / D row group
+
+  // Persistent grid: each workgroup walks tiles blockIdx.x, +gridDim.x, ...
+  // so the per-lane constants above are loaded once per workgroup.
+  int lo = 0;
+  for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+  int hi = n_items - 1;  // items are sorted by tile_off; tiles only grow
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (items[mid].tile_off <= tile) lo = mid;
+    else hi = mid - 1;
+  }
+  const Item it = items[lo];
+  const int T = it.T;
+  const int f0 = (tile - it.tile_off) * kTile;
+  const float* x = samples + it.start;
+  const int64_t L = it.len;
+  float* o = out + it.out_off;
+
+  for (int p = 0; p < kPasses; ++p) {
+    // ---- 1. preemphasised, zero-padded samples of this wave's 4 frames
+    // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
+    // src/frontend.rs:157 computes it), zero outside [0, L).
+    const int fw = f0 + p * kPassFrames + 4 * w;
+    {
+      // Span sample j is item sample s0 + j; valid j lie in [jlo, jhi).
+      // Lane L handles samples 4L + 256 h + (0..3) with one 16-byte load
+      // (global memory needs only dword alignment) and takes x[j - 1] for
+      // its first sample from lane L - 1 with a DPP wave shift.
+      const int64_t s0 = (int64_t)fw * kHop - kPad;
+      const int jlo = s0 < 0 ? (int)(-s0) : 0;
+      const int jhi = (int)(L - s0 < (int64_t)kSpan ? L - s0 : (int64_t)kSpan);
+      const float* xb = x + s0;
+      // x[s0 - 1], the sample before the span, when it exists
+      const float xm1 = (s0 >= 1 && s0 <= L) ? xb[-1] : 0.0f;
+      float4 v4[kSpanVec];
+#pragma unroll
+      for (int h = 0; h < kSpanVec; ++h) {
+        const int j = 4 * lane + 256 * h;
+        if (j >= jlo && j + 3 < jhi) {
+          v4[h] = *reinterpret_cast<const float4*>(xb + j);
+        } else {
+          const int c0 = j < jlo ? jlo : (j >= jhi ? jhi - 1 : j);
+          const int c1 = j + 1 < jlo ? jlo : (j + 1 >= jhi ? jhi - 1 : j + 1);
+          const int c2 = j + 2 < jlo ? jlo : (j + 2 >= jhi ? jhi - 1 : j + 2);
+          const int c3 = j + 3 < jlo ? jlo : (j + 3 >= jhi ? jhi - 1 : j + 3);
+          v4[h] = jhi > jlo ? make_float4(xb[c0], xb[c1], xb[c2], xb[c3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < kSpanVec; ++h) {
+        const int j = 4 * lane + 256 * h;
+        // x[j - 1]: lane L - 1's last sample; lane 0 takes the previous
+        // vector's lane 63 (or the sample before the span).
+        const float edge = h == 0 ? xm1 : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v4[h - 1].w), 63));
+        const float p0 = __int_as_float(
+            __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(v4[h].w), 0x138, 0xf, 0xf, false));
+        const float in[4] = {v4[h].x, v4[h].y, v4[h].z, v4[h].w};
+        const float pv[4] = {p0, v4[h].x, v4[h].y, v4[h].z};
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int je = j + e;
+          // item sample 0 (je == jlo with the span starting before the item)
+          float v = (je == jlo && s0 <= 0) ? in[e] : __fsub_rn(in[e], __fmul_rn(coef, pv[e]));
+          y[e] = (je >= jlo && je < jhi) ? v : 0.0f;
+        }
+        if (j < kSpan) *reinterpret_cast<float4*>(sb + j) = make_float4(y[0], y[1], y[2], y[3]);
+      }
+    }
+    wave_lds_sync();
+
+    // ---- 2. 512-point real FFT of frame g: lane l owns z[l + 16 m2]
+    const float* sp = sb + g * kHop + 2 * l;
     cf a[16];
 #pragma unroll
     for (int m2 = 0; m2 < 12; ++m2) {
-      float2 s = *reinterpret_cast<const float2*>(sp + 32 * m2);
-      a[m2] = {s.x * wv[m2].x, s.y * wv[m2].y};
+      float2 v = *reinterpret_cast<const float2*>(sp + 32 * m2);
+      a[m2] = {v.x * wv[m2].x, v.y * wv[m2].y};
     }
     {
-      float2 s = make_float2(0.0f, 0.0f);
-      if (l < 8) s = *reinterpret_cast<const float2*>(sp + 384);
-      a[12] = {s.x * wv[12].x, s.y * wv[12].y};
+      float2 v = make_float2(0.0f, 0.0f);
+      if (l < 8) v = *reinterpret_cast<const float2*>(sp + 384);
+      a[12] = {v.x * wv[12].x, v.y * wv[12].y};
     }
     a[13] = a[14] = a[15] = {0.0f, 0.0f};
+    wave_lds_sync();  // the transpose below reuses the span's LDS
     dft16<true>(a);
 #pragma unroll
     for (int k1 = 1; k1 < 16; ++k1) a[k1] = cmul(a[k1], t256[k1]);
-    // transpose: row k1, column l
 #pragma unroll
     for (int k1 = 0; k1 < 16; ++k1) X[k1 * kXStride + l] = a[k1];
     wave_lds_sync();
@@ -219,22 +318,20 @@ __global__ __launch_bounds__(kThreads) void sfe_logmel_kernel(const float* __res
 
     // Split partner Z[256 - k] for k = l + 16 k2 lives in lane 16 - l,
     // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).
-    cf b[9];
+    // 2E = A + conj B, 2O = (A - conj B) / i; X[k] = E + W O, X[256-k] = conj(E - W O);
+    // P holds 4|X|^2 (the 0.25 is folded into the filter weights).
+    float* P = pbuf[p & 1][4 * w + g];
 #pragma unroll
     for (int k2 = 0; k2 < 9; ++k2) {
-      cf src = a[(15 - k2) & 15];
-      cf sh = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
-      cf own = a[(16 - k2) & 15];
-      b[k2] = (l == 0) ? own : sh;
-    }
-    wave_lds_sync();
-    // 2E = A + conj B, 2O = (A - conj B) / i; X[k] = E + W O, X[256-k] = conj(E - W O).
-#pragma unroll
-    for (int k2 = 0; k2 < 9; ++k2) {
-      cf A = a[k2], B = b[k2];
+      // Split partner Z[256 - k] for k = l + 16 k2 lives in lane 16 - l,
+      // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).
+      const cf src = a[(15 - k2) & 15];
+      const cf sh = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
+      const cf A = a[k2];
+      const cf B = (l == 0) ? a[(16 - k2) & 15] : sh;
       cf e = {A.x + B.x, A.y - B.y};
-      cf o = {A.y + B.y, B.x - A.x};
-      cf t = cmul(o, t512[k2]);
+      cf od = {A.y + B.y, B.x - A.x};
+      cf t = cmul(od, t512[k2]);
       cf xp = cadd(e, t), xm = csub(e, t);
       float pp = xp.x * xp.x + xp.y * xp.y;
       float pm = xm.x * xm.x + xm.y * xm.y;
@@ -246,27 +343,19 @@ __global__ __launch_bounds__(kThreads) void sfe_logmel_kernel(const float* __res
         P[128] = pp;
       }
     }
-    wave_lds_sync();
-    // mel contraction over each filter's contiguous band, then the guarded log
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int m = l + 16 * i;
-      int cnt = melcnt[m], base = mello[m];
-      const float* w = melw + m * kMelW;
-      float acc = 0.0f;
-      for (int c = 0; c < cnt; ++c) acc = fmaf(w[c], P[base + c], acc);
-      float v = acc + kGuard;
-      lm[m * kLmStride + fr] = (v == kGuard) ? kLnGuard : __log2f(v) * kLn2;
-    }
-    wave_lds_sync();
-  }
-  __syncthreads();
+    __syncthreads();  // all 16 power spectra of this pass are in pbuf[p & 1]
 
-  float* o = out + it.out_off;
-  const int T = it.T;
-  for (int j = tid; j < kMel * kTile; j += kThreads) {
-    int m = j / kTile, t = j % kTile;
-    if (t < nf) o[(int64_t)m * T + f0 + t] = lm[m * kLmStride + t];
+    // ---- 3. mel on the matrix cores: D[filter][frame] += W[filter][4 bins] . P[4 bins][frame]
+    const float* PB = &pbuf[p & 1][n][kk];
+    const int t = f0 + p * kPassFrames + n;
+    float* ot = o + (t < T ? t : 0);
+    switch (w) {
+      case 0: mel_wave<0>(av, k0b, PB, ot, T, t < T, kk); break;
+      case 1: mel_wave<1>(av, k0b, PB, ot, T, t < T, kk); break;
+      case 2: mel_wave<2>(av, k0b, PB, ot, T, t < T, kk); break;
+      default: mel_wave<3>(av, k0b, PB, ot, T, t < T, kk); break;
+    }
+  }
   }
 }
 
@@ -351,10 +440,11 @@ __global__ __launch_bounds__(kThreads) void sfe_norm_kernel(const float* __restr
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
 
 hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int total_tiles,
-                         const DevTables* tables, float preemph, float* raw_out, hipStream_t stream) {
+                         const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream) {
   if (total_tiles <= 0) return hipSuccess;
-  sfe_logmel_kernel<<<dim3(total_tiles), dim3(kThreads), 0, stream>>>(samples, items, n_items, tables, preemph,
-                                                                       raw_out);
+  const int grid = total_tiles < grid_cap ? total_tiles : grid_cap;
+  sfe_logmel_kernel<<<dim3(grid), dim3(kThreads), 0, stream>>>(samples, items, n_items, total_tiles, tables, preemph,
+                                                                raw_out);
   return hipGetLastError();
 }
 

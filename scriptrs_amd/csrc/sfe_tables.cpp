@@ -8,6 +8,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "sfe_internal.hpp"
@@ -73,26 +74,33 @@ bool build_dev_tables(int sample_rate, DevTables* t) {
   }
   std::vector<float> fb((size_t)kMel * kBins);
   mel_filterbank(kNfft, kMel, sample_rate, fb.data());
-  for (int m = 0; m < kMel; ++m) {
-    const float* row = &fb[(size_t)m * kBins];
+  // 16-filter blocks: the first bin (multiple of 4) is chosen here; the
+  // block's nonzero bins must fit the compiled step count.
+  for (int b = 0; b < kBlocks; ++b) {
     int lo = -1, hi = -1;
-    for (int k = 0; k < kBins; ++k)
-      if (row[k] != 0.0f) {
-        if (lo < 0) lo = k;
-        hi = k;
-      }
-    if (lo < 0) {  // an all-zero filter contributes nothing
-      t->mel_lo[m] = 0;
-      t->mel_cnt[m] = 0;
-      continue;
+    for (int m = 16 * b; m < 16 * b + 16; ++m)
+      for (int k = 0; k < kBins; ++k)
+        if (fb[(size_t)m * kBins + k] != 0.0f) {
+          if (lo < 0 || k < lo) lo = k;
+          if (k > hi) hi = k;
+        }
+    if (lo < 0) lo = hi = 0;
+    const int k0 = lo / 4 * 4;
+    if (hi >= k0 + 4 * kBlockSteps[b]) return false;  // filters too wide for this schedule
+    if (k0 + 4 * kBlockSteps[b] > kBins) return false;            // reads stay within the 257 bins
+    t->block_k0[b] = k0;
+  }
+  for (int w = 0; w < kWaves; ++w) {
+    int s = 0;
+    for (int i = 0; i < 3; ++i) {
+      const int b = kWaveBlocks[w][i];
+      if (b < 0) continue;
+      for (int j = 0; j < kBlockSteps[b]; ++j, ++s)
+        for (int L = 0; L < 64; ++L) {
+          int m = 16 * b + L % 16, k = t->block_k0[b] + 4 * j + L / 16;
+          t->a[w][s][L] = fb[(size_t)m * kBins + k] * 0.25f;
+        }
     }
-    int cnt = hi - lo + 1;
-    if (cnt > kMelW) return false;
-    t->mel_lo[m] = lo;
-    t->mel_cnt[m] = cnt;
-    // x0.25 is exact (power of two) and undoes the 4x of the kernel's
-    // unscaled even/odd split.
-    for (int c = 0; c < cnt; ++c) t->mel_w[m * kMelW + c] = row[lo + c] * 0.25f;
   }
   return true;
 }
