@@ -372,11 +372,31 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-// One wavefront per (item, feature) row.  Statistics are exact (f64) for
-// ordinary rows.  A row whose values are all bitwise equal is where the
-// reference's sequential f32 sums decide the result (their rounding leaves
-// x - mean != 0, e.g. about +-0.93 for digital silence); lane 0 replays
-// those sums in the reference's order so such rows match it bit for bit.
+// Statistics of a row whose values are all bitwise equal to x0.  This is
+// where the reference's sequential f32 sums decide the result: their
+// rounding leaves x - mean != 0 (about +-0.93 for digital silence), so the
+// sums are replayed on one lane in the reference's order
+// (src/frontend.rs:230-236).
+__device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_out, float* sd_out) {
+  float sum = 0.0f;
+  for (int t = 0; t < T; ++t) sum = __fadd_rn(sum, x0);
+  const float mean = __fdiv_rn(sum, (float)T);
+  const float d = __fsub_rn(x0, mean);
+  float acc = 0.0f;
+  for (int t = 0; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(d, d));
+  const float var = __fdiv_rn(acc, __fsub_rn((float)T, 1.0f));
+  *mean_out = mean;
+  *sd_out = __fadd_rn(__fsqrt_rn(var), 1e-5f);
+}
+
+constexpr int kRowRegs = 32;  // rows up to 64 * 32 = 2048 frames stay in registers
+
+// normalize_columns (src/frontend.rs:225-241) for one (item, feature) row per
+// wavefront.  Ordinary rows use exact statistics: the mean and the sum of
+// squared deviations are accumulated in f64, then
+// out = (x - mean) / (sqrt(var) + 1e-5) in f32, with var over T - 1 (T == 1
+// gives NaN, as the reference).  Rows of up to 2048 frames are read from
+// HBM once and held in registers; longer rows are streamed three times.
 __global__ __launch_bounds__(kThreads) void sfe_norm_kernel(const float* __restrict__ raw,
                                                             const Item* __restrict__ items, int n_items,
                                                             float* __restrict__ out_f32,
@@ -389,47 +409,78 @@ __global__ __launch_bounds__(kThreads) void sfe_norm_kernel(const float* __restr
   const int T = it.T;
   const int64_t off = it.out_off + (int64_t)m * T;
   const float* x = raw + off;
-
   const float x0 = x[0];
+
+  float meanf, sdf;
+  if (T <= 64 * kRowRegs) {
+    float v[kRowRegs];
+#pragma unroll
+    for (int i = 0; i < kRowRegs; ++i) {
+      const int t = lane + 64 * i;
+      v[i] = t < T ? x[t] : x0;  // padding with x0 keeps the constancy test exact
+    }
+    double s = 0.0;
+    bool eq = true;
+#pragma unroll
+    for (int i = 0; i < kRowRegs; ++i) {
+      if (lane + 64 * i < T) s += (double)v[i];
+      eq = eq && (v[i] == x0);
+    }
+    if (__all(eq)) {
+      float r0 = 0.0f, r1 = 0.0f;
+      if (lane == 0) constant_row_stats(x0, T, &r0, &r1);
+      meanf = __shfl(r0, 0, 64);
+      sdf = __shfl(r1, 0, 64);
+    } else {
+      const double mean = wave_sum(s) / (double)T;
+      double q = 0.0;
+#pragma unroll
+      for (int i = 0; i < kRowRegs; ++i) {
+        const double d = (double)v[i] - mean;
+        if (lane + 64 * i < T) q += d * d;
+      }
+      const double var = wave_sum(q) / (double)(T - 1);
+      meanf = (float)mean;
+      sdf = __fadd_rn(__fsqrt_rn((float)var), 1e-5f);
+    }
+#pragma unroll
+    for (int i = 0; i < kRowRegs; ++i) {
+      const int t = lane + 64 * i;
+      if (t < T) {
+        const float y = __fdiv_rn(__fsub_rn(v[i], meanf), sdf);
+        if (out_bf16) out_bf16[off + t] = f32_to_bf16(y);
+        else out_f32[off + t] = y;
+      }
+    }
+    return;
+  }
+
+  // long rows: three streaming passes
   double s = 0.0;
   bool eq = true;
   for (int t = lane; t < T; t += 64) {
-    float v = x[t];
+    const float v = x[t];
     s += (double)v;
     eq = eq && (v == x0);
   }
-  const bool constant = __all(eq);
-  float meanf, sdf;
-  if (constant) {
+  if (__all(eq)) {
     float r0 = 0.0f, r1 = 0.0f;
-    if (lane == 0) {
-      float sum = 0.0f;
-      for (int t = 0; t < T; ++t) sum = __fadd_rn(sum, x0);
-      float mean = __fdiv_rn(sum, (float)T);
-      float d = __fsub_rn(x0, mean);
-      float acc = 0.0f;
-      for (int t = 0; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(d, d));
-      float var = __fdiv_rn(acc, __fsub_rn((float)T, 1.0f));
-      r0 = mean;
-      r1 = __fadd_rn(__fsqrt_rn(var), 1e-5f);
-    }
+    if (lane == 0) constant_row_stats(x0, T, &r0, &r1);
     meanf = __shfl(r0, 0, 64);
     sdf = __shfl(r1, 0, 64);
   } else {
-    s = wave_sum(s);
-    const double mean = s / (double)T;
+    const double mean = wave_sum(s) / (double)T;
     double q = 0.0;
     for (int t = lane; t < T; t += 64) {
-      double d = (double)x[t] - mean;
+      const double d = (double)x[t] - mean;
       q += d * d;
     }
-    q = wave_sum(q);
-    const double var = q / (double)(T - 1);  // T == 1 gives NaN, as the reference
+    const double var = wave_sum(q) / (double)(T - 1);
     meanf = (float)mean;
     sdf = __fadd_rn(__fsqrt_rn((float)var), 1e-5f);
   }
   for (int t = lane; t < T; t += 64) {
-    float y = __fdiv_rn(__fsub_rn(x[t], meanf), sdf);
+    const float y = __fdiv_rn(__fsub_rn(x[t], meanf), sdf);
     if (out_bf16) out_bf16[off + t] = f32_to_bf16(y);
     else out_f32[off + t] = y;
   }
