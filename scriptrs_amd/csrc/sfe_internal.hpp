@@ -24,7 +24,7 @@ constexpr int kPad = kNfft / 2;       // 256 zeros each side (src/frontend.rs:12
 constexpr int kWaves = 4;
 constexpr int kBlocks = kMel / 16;
 constexpr int kBlockSteps[kBlocks] = {4, 4, 4, 5, 8, 11, 15, 22};
-constexpr int kWaveBlocks[kWaves][3] = {{7, -1, -1}, {6, 0, -1}, {5, 3, 1}, {4, 2, -1}};
+constexpr int kWaveBlocks[kWaves][3] = {{7, -1, -1}, {6, -1, -1}, {5, 3, 0}, {4, 2, 1}};
 constexpr int wave_steps(int w) {
   int n = 0;
   for (int i = 0; i < 3; ++i)

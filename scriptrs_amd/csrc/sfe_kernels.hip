@@ -135,6 +135,39 @@ static_assert(kSpan <= kWaveBuf, "span must fit the wave buffer");
 constexpr int kSpanVec = (kSpan + 255) / 256;  // 16-byte loads per lane (4)
 static_assert(kSpan % 4 == 0, "span is whole float4s");
 
+// The 880 samples under one wave's 4 frames of a unit: span sample j is
+// item sample s0 + j, valid for j in [jlo, jhi).
+struct Span {
+  const float* xb;
+  int64_t s0;
+  int jlo, jhi;
+  bool interior;  // the whole span lies inside the item, after its first sample
+};
+
+__device__ __forceinline__ Span make_span(const Item& it, const float* samples, int u, int w) {
+  const int f0 = (u / kPasses - it.tile_off) * kTile;
+  const int fw = f0 + (u % kPasses) * kPassFrames + 4 * w;
+  Span sp;
+  sp.s0 = (int64_t)fw * kHop - kPad;
+  sp.jlo = sp.s0 < 0 ? (int)(-sp.s0) : 0;
+  sp.jhi = (int)(it.len - sp.s0 < (int64_t)kSpan ? (it.len - sp.s0 > 0 ? it.len - sp.s0 : 0) : (int64_t)kSpan);
+  sp.xb = samples + it.start + sp.s0;
+  sp.interior = sp.jlo == 0 && sp.jhi == kSpan && sp.s0 > 0;
+  return sp;
+}
+
+// Issues the 16-byte loads of an interior span (lane L: samples 4L + 256 h
+// + 0..3) and of the sample before it.  Other spans are read when processed.
+__device__ __forceinline__ void prefetch_span(const Span& sp, int lane, float4 (&v)[kSpanVec], float& xm1) {
+  if (!sp.interior) return;
+#pragma unroll
+  for (int h = 0; h < kSpanVec; ++h) {
+    const int j = 4 * lane + 256 * h;
+    v[h] = *reinterpret_cast<const float4*>(sp.xb + (j < kSpan ? j : 0));
+  }
+  xm1 = sp.xb[-1];
+}
+
 // Guarded log (src/frontend.rs:111-113): ln(v + 2^-24), with the exact
 // f32 value of ln(2^-24) when the mel value adds nothing to the guard.
 __device__ __forceinline__ float guarded_log(float v) {
@@ -142,33 +175,54 @@ __device__ __forceinline__ float guarded_log(float v) {
   return (u == kGuard) ? kLnGuard : __log2f(u) * kLn2;
 }
 
-// One filter block on the matrix cores: all B operands are read first (one
-// LDS wait), then the block's MFMA chain runs back to back.  Lane (n, kk)
-// ends with D[4 kk + r][n]: filters 16 b + 4 kk + r of frame n.
+// Independent accumulator chains per block: a long block's steps alternate
+// between chains so consecutive MFMAs do not wait on each other.
 template <int B>
-__device__ __forceinline__ void mel_block(const float* av, int k0, const float* PB, float* ot, int T, bool valid,
-                                          int kk) {
+constexpr int block_chains() {
+  return kBlockSteps[B] >= 16 ? 3 : (kBlockSteps[B] >= 8 ? 2 : 1);
+}
+
+// MFMA chains of one filter block.  All B operands of the block are read
+// first (one LDS wait).  Lane (n, kk) ends with D[4 kk + r][n]: filters
+// 16 B + 4 kk + r of frame n.
+template <int B>
+__device__ __forceinline__ f32x4 mel_block(const float* av, int k0, const float* PB) {
   constexpr int S = kBlockSteps[B];
+  constexpr int NC = block_chains<B>();
   float bv[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) bv[s] = PB[k0 + 4 * s];
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[NC];
 #pragma unroll
-  for (int s = 0; s < S; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
-  if (valid) {
-    float* row = ot + (int64_t)(16 * B + 4 * kk) * T;
+  for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) row[(int64_t)r * T] = guarded_log(acc[r]);
-  }
+  for (int s = 0; s < S; ++s) acc[s % NC] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc[s % NC], 0, 0, 0);
+#pragma unroll
+  for (int c = 1; c < NC; ++c) acc[0] += acc[c];
+  return acc[0];
 }
 
+__device__ __forceinline__ void store_block(const f32x4& acc, int b, float* ot, int T, int kk) {
+  float* row = ot + (int64_t)(16 * b + 4 * kk) * T;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) row[(int64_t)r * T] = guarded_log(acc[r]);
+}
+
+// All of a wave's blocks: the chains run in one branch-free region so the
+// scheduler can interleave them; the guarded logs and stores follow.
 template <int W>
 __device__ __forceinline__ void mel_wave(const float (&av)[kMaxSteps], const int (&k0b)[kBlocks], const float* PB,
                                          float* ot, int T, bool valid, int kk) {
   constexpr int b0 = kWaveBlocks[W][0], b1 = kWaveBlocks[W][1], b2 = kWaveBlocks[W][2];
-  mel_block<b0>(av, k0b[b0], PB, ot, T, valid, kk);
-  if constexpr (b1 >= 0) mel_block<b1>(av + kBlockSteps[b0], k0b[b1], PB, ot, T, valid, kk);
-  if constexpr (b2 >= 0) mel_block<b2>(av + kBlockSteps[b0] + kBlockSteps[b1], k0b[b2], PB, ot, T, valid, kk);
+  const f32x4 d0 = mel_block<b0>(av, k0b[b0], PB);
+  f32x4 d1, d2;
+  if constexpr (b1 >= 0) d1 = mel_block<b1>(av + kBlockSteps[b0], k0b[b1], PB);
+  if constexpr (b2 >= 0) d2 = mel_block<b2>(av + kBlockSteps[b0] + kBlockSteps[b1], k0b[b2], PB);
+  if (valid) {
+    store_block(d0, b0, ot, T, kk);
+    if constexpr (b1 >= 0) store_block(d1, b1, ot, T, kk);
+    if constexpr (b2 >= 0) store_block(d2, b2, ot, T, kk);
+  }
 }
 
 __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __restrict__ samples,
@@ -221,87 +275,103 @@ __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __
   const int n = lane & 15;        // MFMA: B column (frame) / D column
   const int kk = lane >> 4;       // MFMA: B row (bin within the step) / D row group
 
-  // Persistent grid: each workgroup walks tiles blockIdx.x, +gridDim.x, ...
-  // so the per-lane constants above are loaded once per workgroup.
-  int lo = 0;
-  for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
-  int hi = n_items - 1;  // items are sorted by tile_off; tiles only grow
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (items[mid].tile_off <= tile) lo = mid;
-    else hi = mid - 1;
+  // Persistent grid: each workgroup walks one contiguous range of tiles, so
+  // the per-lane constants above are loaded once per workgroup and
+  // neighbouring tiles (which share cache lines of the output rows and of
+  // the input) stay on one XCD's L2.
+  const int t_begin = (int)((int64_t)total_tiles * blockIdx.x / gridDim.x);
+  const int t_end = (int)((int64_t)total_tiles * (blockIdx.x + 1) / gridDim.x);
+  // Units are (tile, pass) pairs, processed in order.  The samples of unit
+  // u + 1 are loaded into registers while unit u is transformed, so the
+  // global-load latency hides behind the FFT.
+  const int u_begin = t_begin * kPasses, u_end = t_end * kPasses;
+  int li_n = 0;  // item of the unit being prefetched
+  {
+    int hi = n_items - 1;
+    while (li_n < hi) {
+      int mid = (li_n + hi + 1) >> 1;
+      if (items[mid].tile_off <= t_begin) li_n = mid;
+      else hi = mid - 1;
+    }
   }
-  const Item it = items[lo];
-  const int T = it.T;
-  const int f0 = (tile - it.tile_off) * kTile;
-  const float* x = samples + it.start;
-  const int64_t L = it.len;
-  float* o = out + it.out_off;
+  Span sp_n = make_span(items[li_n], samples, u_begin, w);
+  float4 nv[kSpanVec];
+  float nxm1 = 0.0f;
+  prefetch_span(sp_n, lane, nv, nxm1);
 
-  for (int p = 0; p < kPasses; ++p) {
+  for (int u = u_begin; u < u_end; ++u) {
+    const int li = li_n;
+    const Span sp = sp_n;
+    float4 cv[kSpanVec];
+#pragma unroll
+    for (int h = 0; h < kSpanVec; ++h) cv[h] = nv[h];
+    const float cxm1 = nxm1;
+    if (u + 1 < u_end) {
+      const int tile_n = (u + 1) / kPasses;
+      while (li_n + 1 < n_items && items[li_n + 1].tile_off <= tile_n) ++li_n;
+      sp_n = make_span(items[li_n], samples, u + 1, w);
+      prefetch_span(sp_n, lane, nv, nxm1);
+    }
+    const Item it = items[li];
+    const int T = it.T;
+    const int p = u % kPasses;
+    const int f0 = (u / kPasses - it.tile_off) * kTile;
+    float* o = out + it.out_off;
+
     // ---- 1. preemphasised, zero-padded samples of this wave's 4 frames
     // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
     // src/frontend.rs:157 computes it), zero outside [0, L).
-    const int fw = f0 + p * kPassFrames + 4 * w;
-    {
-      // Span sample j is item sample s0 + j; valid j lie in [jlo, jhi).
-      // Lane L handles samples 4L + 256 h + (0..3) with one 16-byte load
-      // (global memory needs only dword alignment) and takes x[j - 1] for
-      // its first sample from lane L - 1 with a DPP wave shift.
-      const int64_t s0 = (int64_t)fw * kHop - kPad;
-      const int jlo = s0 < 0 ? (int)(-s0) : 0;
-      const int jhi = (int)(L - s0 < (int64_t)kSpan ? L - s0 : (int64_t)kSpan);
-      const float* xb = x + s0;
-      // x[s0 - 1], the sample before the span, when it exists
-      const float xm1 = (s0 >= 1 && s0 <= L) ? xb[-1] : 0.0f;
-      float4 v4[kSpanVec];
-#pragma unroll
-      for (int h = 0; h < kSpanVec; ++h) {
-        const int j = 4 * lane + 256 * h;
-        if (j >= jlo && j + 3 < jhi) {
-          v4[h] = *reinterpret_cast<const float4*>(xb + j);
-        } else {
-          const int c0 = j < jlo ? jlo : (j >= jhi ? jhi - 1 : j);
-          const int c1 = j + 1 < jlo ? jlo : (j + 1 >= jhi ? jhi - 1 : j + 1);
-          const int c2 = j + 2 < jlo ? jlo : (j + 2 >= jhi ? jhi - 1 : j + 2);
-          const int c3 = j + 3 < jlo ? jlo : (j + 3 >= jhi ? jhi - 1 : j + 3);
-          v4[h] = jhi > jlo ? make_float4(xb[c0], xb[c1], xb[c2], xb[c3]) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
+    if (sp.interior) {
 #pragma unroll
       for (int h = 0; h < kSpanVec; ++h) {
         const int j = 4 * lane + 256 * h;
         // x[j - 1]: lane L - 1's last sample; lane 0 takes the previous
         // vector's lane 63 (or the sample before the span).
-        const float edge = h == 0 ? xm1 : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v4[h - 1].w), 63));
+        const float edge = h == 0 ? cxm1 : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv[h - 1].w), 63));
         const float p0 = __int_as_float(
-            __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(v4[h].w), 0x138, 0xf, 0xf, false));
-        const float in[4] = {v4[h].x, v4[h].y, v4[h].z, v4[h].w};
-        const float pv[4] = {p0, v4[h].x, v4[h].y, v4[h].z};
-        float y[4];
+            __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(cv[h].w), 0x138, 0xf, 0xf, false));
+        float4 y;
+        y.x = __fsub_rn(cv[h].x, __fmul_rn(coef, p0));
+        y.y = __fsub_rn(cv[h].y, __fmul_rn(coef, cv[h].x));
+        y.z = __fsub_rn(cv[h].z, __fmul_rn(coef, cv[h].y));
+        y.w = __fsub_rn(cv[h].w, __fmul_rn(coef, cv[h].z));
+        if (j < kSpan) *reinterpret_cast<float4*>(sb + j) = y;
+      }
+    } else {
+      // span crossing the item's start or end: per-sample bounds
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int je = j + e;
-          // item sample 0 (je == jlo with the span starting before the item)
-          float v = (je == jlo && s0 <= 0) ? in[e] : __fsub_rn(in[e], __fmul_rn(coef, pv[e]));
-          y[e] = (je >= jlo && je < jhi) ? v : 0.0f;
+      for (int h = 0; h < kSpanVec; ++h) {
+        const int j = 4 * lane + 256 * h;
+        if (j < kSpan) {
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int je = j + e;
+            float v = 0.0f;
+            if (je >= sp.jlo && je < sp.jhi) {
+              const float cur = sp.xb[je];
+              // item sample 0 (je == jlo with the span starting before the item)
+              v = (je == sp.jlo && sp.s0 <= 0) ? cur : __fsub_rn(cur, __fmul_rn(coef, sp.xb[je - 1]));
+            }
+            y[e] = v;
+          }
+          *reinterpret_cast<float4*>(sb + j) = make_float4(y[0], y[1], y[2], y[3]);
         }
-        if (j < kSpan) *reinterpret_cast<float4*>(sb + j) = make_float4(y[0], y[1], y[2], y[3]);
       }
     }
     wave_lds_sync();
 
     // ---- 2. 512-point real FFT of frame g: lane l owns z[l + 16 m2]
-    const float* sp = sb + g * kHop + 2 * l;
+    const float* fin = sb + g * kHop + 2 * l;
     cf a[16];
 #pragma unroll
     for (int m2 = 0; m2 < 12; ++m2) {
-      float2 v = *reinterpret_cast<const float2*>(sp + 32 * m2);
+      float2 v = *reinterpret_cast<const float2*>(fin + 32 * m2);
       a[m2] = {v.x * wv[m2].x, v.y * wv[m2].y};
     }
     {
       float2 v = make_float2(0.0f, 0.0f);
-      if (l < 8) v = *reinterpret_cast<const float2*>(sp + 384);
+      if (l < 8) v = *reinterpret_cast<const float2*>(fin + 384);
       a[12] = {v.x * wv[12].x, v.y * wv[12].y};
     }
     a[13] = a[14] = a[15] = {0.0f, 0.0f};
@@ -355,7 +425,6 @@ __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __
       case 2: mel_wave<2>(av, k0b, PB, ot, T, t < T, kk); break;
       default: mel_wave<3>(av, k0b, PB, ot, T, t < T, kk); break;
     }
-  }
   }
 }
 
