@@ -61,6 +61,8 @@ def main() -> int:
     ap.add_argument("--workload", default="config3", choices=["config1", "config2", "config3", "config4"])
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB per step (calibrates the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -68,6 +70,15 @@ def main() -> int:
         return 2
 
     import torch
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": 4 * n, "bytes_written": 4 * n}), flush=True)
+        return 0
     from scriptrs_amd import ParakeetFeatureExtractor, _lib
 
     x, tasks, desc = make_workload(args.workload)
