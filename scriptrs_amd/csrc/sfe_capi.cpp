@@ -123,7 +123,7 @@ struct sfe_ctx {
   hipStream_t s_copy = nullptr;
   DevBuf meta;      // Item tables
   PinBuf h_meta;
-  DevBuf scratch;   // f32 raw log-mel for bf16 output
+  DevBuf scratch;   // raw log-mel, frame-major f32 (the normalisation kernel's input)
   DevBuf io_in;     // sfe_extract staging (audio)
   DevBuf io_out;    // sfe_extract staging (features)
   DevBuf win[2];    // streamed windows
@@ -174,8 +174,8 @@ hipEvent_t timing_event(sfe_ctx* ctx) {
 
 // Launches the log-mel kernel then the normalisation kernel; with timing on,
 // brackets each with events (read back by sfe_get_timing).
-int launch_pair(sfe_ctx* ctx, const float* samples, const Item* d_items, int n, int tiles, float* raw, void* out,
-                int32_t out_dtype, hipStream_t stream) {
+int launch_pair(sfe_ctx* ctx, const float* samples, const Item* d_items, int n, int tiles, int max_T, float* raw,
+                void* out, int32_t out_dtype, hipStream_t stream) {
   hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
   if (ctx->timing)
     for (int i = 0; i < 4; ++i)
@@ -184,7 +184,7 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* d_items, int n, 
   SFE_HIP(sfe::launch_logmel(samples, d_items, n, tiles, ctx->d_tables, ctx->cfg.preemphasis, raw, ctx->grid_cap, stream));
   if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
   if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
-  SFE_HIP(sfe::launch_norm(raw, d_items, n, out, out_dtype == SFE_BF16, stream));
+  SFE_HIP(sfe::launch_norm(raw, d_items, n, max_T, out, out_dtype == SFE_BF16, stream));
   if (e[3]) SFE_HIP(hipEventRecord(e[3], stream));
   return SFE_OK;
 }
@@ -201,12 +201,11 @@ int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items
   SFE_HIP(hipEventRecord(ctx->h_meta.ev, stream));
   ctx->h_meta.pending = true;
   const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
-  float* raw = static_cast<float*>(out);
-  if (out_dtype == SFE_BF16) {
-    SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
-    raw = static_cast<float*>(ctx->scratch.ptr);
-  }
-  return launch_pair(ctx, samples, d_items, (int)items.size(), (int)total_tiles, raw, out, out_dtype, stream);
+  SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
+  float* raw = static_cast<float*>(ctx->scratch.ptr);
+  int max_T = 0;
+  for (const Item& it : items) max_T = std::max(max_T, (int)it.T);
+  return launch_pair(ctx, samples, d_items, (int)items.size(), (int)total_tiles, max_T, raw, out, out_dtype, stream);
 }
 
 int check_ctx(sfe_ctx* ctx) {
@@ -463,11 +462,11 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
   struct Group {
     int32_t first, count;
     int64_t wstart, wend;
-    int32_t tiles;
+    int32_t tiles, max_T;
   };
   std::vector<Group> groups;
   for (int32_t i = 0; i < n;) {
-    Group g{i, 0, items[i].start, items[i].start, 0};
+    Group g{i, 0, items[i].start, items[i].start, 0, 0};
     while (i < n && items[i].start + items[i].len - g.wstart <= window_samples) {
       g.wend = std::max(g.wend, items[i].start + items[i].len);
       ++i;
@@ -481,17 +480,15 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
       items[i].start -= g.wstart;
       items[i].tile_off = t;
       t += (int32_t)sfe::tiles_for(items[i].T);
+      g.max_T = std::max(g.max_T, (int)items[i].T);
     }
     g.tiles = t;
   }
   const size_t mbytes = items.size() * sizeof(Item);
   SFE_HIP(ctx->h_meta.reserve(mbytes));
   SFE_HIP(ctx->meta.reserve(mbytes));
-  float* raw = static_cast<float*>(out);
-  if (out_dtype == SFE_BF16) {
-    SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
-    raw = static_cast<float*>(ctx->scratch.ptr);
-  }
+  SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
+  float* raw = static_cast<float*>(ctx->scratch.ptr);
   for (int b = 0; b < 2; ++b) {
     SFE_HIP(ctx->win[b].reserve((size_t)window_samples * sizeof(float)));
     SFE_HIP(ctx->h_win[b].reserve((size_t)window_samples * sizeof(float)));
@@ -517,7 +514,7 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
     ctx->h_win[b].pending = true;
     SFE_HIP(hipEventRecord(ctx->ev_copied[b], sx));
     SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[b], 0));
-    rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), d_items + g.first, g.count, g.tiles, raw, out,
+    rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), d_items + g.first, g.count, g.tiles, g.max_T, raw, out,
                      out_dtype, sc);
     if (rc) return rc;
     SFE_HIP(hipEventRecord(ctx->ev_done[b], sc));

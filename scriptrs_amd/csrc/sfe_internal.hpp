@@ -37,13 +37,14 @@ static_assert(wave_steps(0) <= kMaxSteps && wave_steps(1) <= kMaxSteps && wave_s
               "schedule exceeds the per-wave step budget");
 
 // One featurized item: a clip or a long-form chunk task.  samples[start,
-// start+len) is featurized into out[out_off + m*T + t].
+// start+len) is featurized into out[out_off + m*T + t] (raw log-mel in
+// scratch at raw[out_off + t*128 + m]).
 struct Item {
   int64_t start;
   int64_t len;
   int64_t out_off;   // element offset = feature_size * frame_offset
   int32_t T;         // len / hop + 1
-  int32_t tile_off;  // first frame tile of this item, relative to the launch
+  int32_t tile_off;  // first 16-frame unit of this item, relative to the launch
 };
 
 // Constant tables, uploaded once per context.
@@ -65,16 +66,19 @@ void mel_filterbank(int n_fft, int n_mels, int sample_rate, float* out);
 bool build_dev_tables(int sample_rate, DevTables* t);
 
 // Kernel launchers (sfe_kernels.hip).  All asynchronous on `stream`.
-constexpr int kTile = 64;  // frames per workgroup of the log-mel kernel
+constexpr int kTile = 16;  // frames per unit of work (one pass) of the log-mel kernel
 int64_t tiles_for(int64_t T);
 // grid_cap: workgroups resident on the device at once (the kernel loops
 // over tiles, so launching more than that only adds scheduling overhead).
 hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int total_tiles,
                          const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream);
-constexpr int kLogmelBlocksPerCU = 2;
-// Normalises raw (f32, layout as above) per (item, feature) row and writes
-// to out (f32, may alias raw) or bf16 (uint16_t*) when out_bf16 is set.
-hipError_t launch_norm(const float* raw, const Item* items, int n_items, void* out, bool out_bf16,
+constexpr int kLogmelWavesPerSimd = 2;
+constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
+// Normalises raw (f32, frame-major [T][128] per item) per (item, feature)
+// and writes feature-major [128][T] per item to out (f32, must not alias
+// raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
+// frame count (sizes the kernel's register budget).
+hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, void* out, bool out_bf16,
                        hipStream_t stream);
 
 }  // namespace sfe

@@ -1,14 +1,15 @@
 // CDNA4 (gfx950) kernels of the log-mel front end.
 //
-// sfe_logmel_kernel fuses, per tile of 32 frames of one item, everything
+// sfe_logmel_kernel fuses, per pass of 16 frames of one item, everything
 // ParakeetFeatureExtractor::extract does before normalisation
 // (src/frontend.rs:104-147, :150-159):
 //   preemphasis restarted at the item start -> 256-zero padding ->
 //   400-tap left-aligned Hann window -> 512-point real FFT -> |X|^2 ->
 //   128x257 Slaney mel contraction -> ln(x + 2^-24)
-// and writes the raw log-mel feature-major ([128][T] per item).
+// and writes the raw log-mel frame-major ([T][128] per item) to scratch.
 // sfe_norm_kernel then applies normalize_columns (src/frontend.rs:225-241)
-// per (item, feature) row.
+// per (item, feature) and writes the reference's feature-major layout
+// ([128][T] per item).
 //
 // FFT mapping: the 512-point real FFT is a 256-point complex FFT of
 // z[m] = r[2m] + i r[2m+1] followed by the even/odd split.  The 256-point
@@ -119,15 +120,14 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Work of one workgroup: a tile of kTile frames of one item, in passes of 16
-// frames.  In a pass each of the 4 waves transforms 4 consecutive frames (16
-// lanes per frame) and writes their power spectra to the shared P buffer;
-// after one workgroup barrier every wave contracts all 16 frames with its
-// share of the mel filter blocks on the matrix cores and stores the log.
-// P is double-buffered, so the next pass's FFTs overlap this pass's MFMAs
-// and a pass needs a single barrier.
+// Work of one workgroup: a contiguous range of units; a unit is one pass of
+// 16 consecutive frames of one item.  In a pass each of the 4 waves
+// transforms 4 consecutive frames (16 lanes per frame) and writes their
+// power spectra to the shared P buffer; after one workgroup barrier every
+// wave contracts all 16 frames with its share of the mel filter blocks on
+// the matrix cores.  P is double-buffered, so a pass needs a single barrier.
 constexpr int kPassFrames = 16;
-constexpr int kPasses = kTile / kPassFrames;
+static_assert(kTile == kPassFrames, "a unit of work is one 16-frame pass");
 constexpr int kSpan = 3 * kHop + kWin;  // samples under 4 consecutive frames (880)
 constexpr int kWaveBuf = 4 * kSlot * 2; // floats: 4 transpose slots; also holds the 880-sample span
 constexpr int kPStride = 258;           // floats per P row (258 = 2 mod 32: conflict-free B reads)
@@ -145,8 +145,7 @@ struct Span {
 };
 
 __device__ __forceinline__ Span make_span(const Item& it, const float* samples, int u, int w) {
-  const int f0 = (u / kPasses - it.tile_off) * kTile;
-  const int fw = f0 + (u % kPasses) * kPassFrames + 4 * w;
+  const int fw = (u - it.tile_off) * kPassFrames + 4 * w;
   Span sp;
   sp.s0 = (int64_t)fw * kHop - kPad;
   sp.jlo = sp.s0 < 0 ? (int)(-sp.s0) : 0;
@@ -182,50 +181,81 @@ constexpr int block_chains() {
   return kBlockSteps[B] >= 16 ? 3 : (kBlockSteps[B] >= 8 ? 2 : 1);
 }
 
-// MFMA chains of one filter block.  All B operands of the block are read
-// first (one LDS wait).  Lane (n, kk) ends with D[4 kk + r][n]: filters
-// 16 B + 4 kk + r of frame n.
-template <int B>
-__device__ __forceinline__ f32x4 mel_block(const float* av, int k0, const float* PB) {
-  constexpr int S = kBlockSteps[B];
-  constexpr int NC = block_chains<B>();
-  float bv[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) bv[s] = PB[k0 + 4 * s];
-  f32x4 acc[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int s = 0; s < S; ++s) acc[s % NC] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc[s % NC], 0, 0, 0);
-#pragma unroll
-  for (int c = 1; c < NC; ++c) acc[0] += acc[c];
-  return acc[0];
-}
+// One wave's mel results for one pass: D[j] holds block kWaveBlocks[W][j];
+// lane (n, kk) holds filters 16 b + 4 kk + r of frame n.
+struct MelAcc {
+  f32x4 d[3];
+};
 
-__device__ __forceinline__ void store_block(const f32x4& acc, int b, float* ot, int T, int kk) {
-  float* row = ot + (int64_t)(16 * b + 4 * kk) * T;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) row[(int64_t)r * T] = guarded_log(acc[r]);
-}
-
-// All of a wave's blocks: the chains run in one branch-free region so the
-// scheduler can interleave them; the guarded logs and stores follow.
+// MFMA chains of all of a wave's filter blocks for one pass.  Every B
+// operand is read from LDS before the first MFMA is issued (one LDS wait),
+// and the chains of a long block alternate between accumulators so
+// consecutive MFMAs do not wait on each other.  The results are consumed a
+// pass later (mel_store), so the MFMA latency hides behind the next FFT.
 template <int W>
-__device__ __forceinline__ void mel_wave(const float (&av)[kMaxSteps], const int (&k0b)[kBlocks], const float* PB,
-                                         float* ot, int T, bool valid, int kk) {
-  constexpr int b0 = kWaveBlocks[W][0], b1 = kWaveBlocks[W][1], b2 = kWaveBlocks[W][2];
-  const f32x4 d0 = mel_block<b0>(av, k0b[b0], PB);
-  f32x4 d1, d2;
-  if constexpr (b1 >= 0) d1 = mel_block<b1>(av + kBlockSteps[b0], k0b[b1], PB);
-  if constexpr (b2 >= 0) d2 = mel_block<b2>(av + kBlockSteps[b0] + kBlockSteps[b1], k0b[b2], PB);
-  if (valid) {
-    store_block(d0, b0, ot, T, kk);
-    if constexpr (b1 >= 0) store_block(d1, b1, ot, T, kk);
-    if constexpr (b2 >= 0) store_block(d2, b2, ot, T, kk);
+__device__ __forceinline__ void mel_mfma(const float (&av)[kMaxSteps], const int (&k0b)[kBlocks], const float* PB,
+                                         MelAcc& acc) {
+  constexpr int b[3] = {kWaveBlocks[W][0], kWaveBlocks[W][1], kWaveBlocks[W][2]};
+  constexpr int S[3] = {kBlockSteps[b[0]], b[1] >= 0 ? kBlockSteps[b[1] < 0 ? 0 : b[1]] : 0,
+                        b[2] >= 0 ? kBlockSteps[b[2] < 0 ? 0 : b[2]] : 0};
+  constexpr int NS = S[0] + S[1] + S[2];
+  static_assert(NS <= kMaxSteps, "wave step budget");
+  float bv[NS];
+#pragma unroll
+  for (int j = 0, s0 = 0; j < 3; s0 += S[j], ++j)
+#pragma unroll
+    for (int s = 0; s < S[j]; ++s) bv[s0 + s] = PB[k0b[b[j] < 0 ? 0 : b[j]] + 4 * s];
+  __builtin_amdgcn_sched_barrier(0);
+  // Two accumulators per block (three for the longest), interleaved.
+  f32x4 c[3][3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) c[j][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0, s0 = 0; j < 3; s0 += S[j], ++j) {
+#pragma unroll
+    for (int s = 0; s < S[j]; ++s) {
+      const int q = S[j] >= 16 ? s % 3 : (S[j] >= 8 ? s % 2 : 0);
+      c[j][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s0 + s], bv[s0 + s], c[j][q], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (S[j] >= 16) acc.d[j] = c[j][0] + c[j][1] + c[j][2];
+    else if (S[j] >= 8) acc.d[j] = c[j][0] + c[j][1];
+    else acc.d[j] = c[j][0];
   }
 }
 
-__global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __restrict__ samples,
+// Raw log-mel is written frame-major ([T][128] per item): lane (n, kk)
+// holds filters 16 b + 4 kk .. + 3 of frame n, one aligned 16-byte store.
+// The 4 waves of a pass together cover whole 512-byte frame rows.
+__device__ __forceinline__ void store_block(const f32x4& v, int b, float* frame_row, int kk) {
+  *reinterpret_cast<float4*>(frame_row + 16 * b + 4 * kk) =
+      make_float4(guarded_log(v[0]), guarded_log(v[1]), guarded_log(v[2]), guarded_log(v[3]));
+}
+
+template <int W>
+__device__ __forceinline__ void mel_store(const MelAcc& acc, float* frame_row, int kk) {
+  constexpr int b0 = kWaveBlocks[W][0], b1 = kWaveBlocks[W][1], b2 = kWaveBlocks[W][2];
+  store_block(acc.d[0], b0, frame_row, kk);
+  if constexpr (b1 >= 0) store_block(acc.d[1], b1, frame_row, kk);
+  if constexpr (b2 >= 0) store_block(acc.d[2], b2, frame_row, kk);
+}
+
+// Log and store of the previous pass's mel results (pending when valid).
+__device__ __forceinline__ void store_pending(int w, const MelAcc& acc, float* frame_row, bool valid, int kk) {
+  if (!valid) return;
+  switch (w) {
+    case 0: mel_store<0>(acc, frame_row, kk); break;
+    case 1: mel_store<1>(acc, frame_row, kk); break;
+    case 2: mel_store<2>(acc, frame_row, kk); break;
+    default: mel_store<3>(acc, frame_row, kk); break;
+  }
+}
+
+__global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kernel(const float* __restrict__ samples,
                                                               const Item* __restrict__ items, int n_items,
                                                               int total_tiles, const DevTables* __restrict__ tb,
                                                               float coef, float* __restrict__ out) {
@@ -275,47 +305,47 @@ __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __
   const int n = lane & 15;        // MFMA: B column (frame) / D column
   const int kk = lane >> 4;       // MFMA: B row (bin within the step) / D row group
 
-  // Persistent grid: each workgroup walks one contiguous range of tiles, so
-  // the per-lane constants above are loaded once per workgroup and
-  // neighbouring tiles (which share cache lines of the output rows and of
-  // the input) stay on one XCD's L2.
-  const int t_begin = (int)((int64_t)total_tiles * blockIdx.x / gridDim.x);
-  const int t_end = (int)((int64_t)total_tiles * (blockIdx.x + 1) / gridDim.x);
-  // Units are (tile, pass) pairs, processed in order.  The samples of unit
-  // u + 1 are loaded into registers while unit u is transformed, so the
-  // global-load latency hides behind the FFT.
-  const int u_begin = t_begin * kPasses, u_end = t_end * kPasses;
-  int li_n = 0;  // item of the unit being prefetched
+  // Persistent grid: each workgroup walks one contiguous range of units
+  // (16-frame passes of one item), so the per-lane constants above are
+  // loaded once per workgroup and neighbouring units (which share cache
+  // lines of the output rows and of the input) stay on one XCD's L2.
+  const int u_begin = (int)((int64_t)total_tiles * blockIdx.x / gridDim.x);
+  const int u_end = (int)((int64_t)total_tiles * (blockIdx.x + 1) / gridDim.x);
+  if (u_begin >= u_end) return;
+  // Item descriptors stay in scalar registers: it_c is the item of the unit
+  // being prefetched, it_n the item after it, loaded one item ahead so an
+  // item boundary never waits on memory.  Every item spans at least one unit.
+  int li = 0;
   {
     int hi = n_items - 1;
-    while (li_n < hi) {
-      int mid = (li_n + hi + 1) >> 1;
-      if (items[mid].tile_off <= t_begin) li_n = mid;
+    while (li < hi) {
+      int mid = (li + hi + 1) >> 1;
+      if (items[mid].tile_off <= u_begin) li = mid;
       else hi = mid - 1;
     }
   }
-  Span sp_n = make_span(items[li_n], samples, u_begin, w);
+  Item it_c = items[li];
+  Item it_n = items[li + 1 < n_items ? li + 1 : li];
+  // The samples of unit u + 1 are loaded into registers while unit u is
+  // transformed, so the global-load latency hides behind the FFT.
+  Span sp_n = make_span(it_c, samples, u_begin, w);
   float4 nv[kSpanVec];
   float nxm1 = 0.0f;
   prefetch_span(sp_n, lane, nv, nxm1);
 
+  MelAcc acc;
+  float* pend_row = out;
+  bool pend = false;  // acc holds a pass whose log-mel is not yet stored
+
   for (int u = u_begin; u < u_end; ++u) {
-    const int li = li_n;
+    const Item it = it_c;
     const Span sp = sp_n;
     float4 cv[kSpanVec];
 #pragma unroll
     for (int h = 0; h < kSpanVec; ++h) cv[h] = nv[h];
     const float cxm1 = nxm1;
-    if (u + 1 < u_end) {
-      const int tile_n = (u + 1) / kPasses;
-      while (li_n + 1 < n_items && items[li_n + 1].tile_off <= tile_n) ++li_n;
-      sp_n = make_span(items[li_n], samples, u + 1, w);
-      prefetch_span(sp_n, lane, nv, nxm1);
-    }
-    const Item it = items[li];
     const int T = it.T;
-    const int p = u % kPasses;
-    const int f0 = (u / kPasses - it.tile_off) * kTile;
+    const int f0 = (u - it.tile_off) * kPassFrames;
     float* o = out + it.out_off;
 
     // ---- 1. preemphasised, zero-padded samples of this wave's 4 frames
@@ -359,6 +389,20 @@ __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __
         }
       }
     }
+    // The previous pass's log-mel goes out while the span's LDS writes land.
+    store_pending(w, acc, pend_row, pend, kk);
+    // Then the next unit's samples are requested.  Vector memory operations
+    // complete in issue order, so loading after the stores means the wait
+    // for these samples, a pass from now, never waits on fresh stores.
+    if (u + 1 < u_end) {
+      if (li + 1 < n_items && u + 1 >= it_n.tile_off) {
+        ++li;
+        it_c = it_n;
+        it_n = items[li + 1 < n_items ? li + 1 : li];
+      }
+      sp_n = make_span(it_c, samples, u + 1, w);
+      prefetch_span(sp_n, lane, nv, nxm1);
+    }
     wave_lds_sync();
 
     // ---- 2. 512-point real FFT of frame g: lane l owns z[l + 16 m2]
@@ -390,15 +434,18 @@ __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __
     // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).
     // 2E = A + conj B, 2O = (A - conj B) / i; X[k] = E + W O, X[256-k] = conj(E - W O);
     // P holds 4|X|^2 (the 0.25 is folded into the filter weights).
-    float* P = pbuf[p & 1][4 * w + g];
+    // All 18 shuffles are issued before the arithmetic that consumes them.
+    cf sh[9];
 #pragma unroll
     for (int k2 = 0; k2 < 9; ++k2) {
-      // Split partner Z[256 - k] for k = l + 16 k2 lives in lane 16 - l,
-      // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).
       const cf src = a[(15 - k2) & 15];
-      const cf sh = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
+      sh[k2] = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
+    }
+    float* P = pbuf[u & 1][4 * w + g];
+#pragma unroll
+    for (int k2 = 0; k2 < 9; ++k2) {
       const cf A = a[k2];
-      const cf B = (l == 0) ? a[(16 - k2) & 15] : sh;
+      const cf B = (l == 0) ? a[(16 - k2) & 15] : sh[k2];
       cf e = {A.x + B.x, A.y - B.y};
       cf od = {A.y + B.y, B.x - A.x};
       cf t = cmul(od, t512[k2]);
@@ -413,25 +460,21 @@ __global__ __launch_bounds__(kThreads, 2) void sfe_logmel_kernel(const float* __
         P[128] = pp;
       }
     }
-    __syncthreads();  // all 16 power spectra of this pass are in pbuf[p & 1]
+    __syncthreads();  // all 16 power spectra of this pass are in pbuf[u & 1]
 
     // ---- 3. mel on the matrix cores: D[filter][frame] += W[filter][4 bins] . P[4 bins][frame]
-    const float* PB = &pbuf[p & 1][n][kk];
-    const int t = f0 + p * kPassFrames + n;
-    float* ot = o + (t < T ? t : 0);
+    const float* PB = &pbuf[u & 1][n][kk];
     switch (w) {
-      case 0: mel_wave<0>(av, k0b, PB, ot, T, t < T, kk); break;
-      case 1: mel_wave<1>(av, k0b, PB, ot, T, t < T, kk); break;
-      case 2: mel_wave<2>(av, k0b, PB, ot, T, t < T, kk); break;
-      default: mel_wave<3>(av, k0b, PB, ot, T, t < T, kk); break;
+      case 0: mel_mfma<0>(av, k0b, PB, acc); break;
+      case 1: mel_mfma<1>(av, k0b, PB, acc); break;
+      case 2: mel_mfma<2>(av, k0b, PB, acc); break;
+      default: mel_mfma<3>(av, k0b, PB, acc); break;
     }
+    const int t = f0 + n;
+    pend = t < T;
+    pend_row = o + (int64_t)(pend ? t : 0) * kMel;
   }
-}
-
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  store_pending(w, acc, pend_row, pend, kk);
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
@@ -458,100 +501,274 @@ __device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_
   *sd_out = __fadd_rn(__fsqrt_rn(var), 1e-5f);
 }
 
-constexpr int kRowRegs = 32;  // rows up to 64 * 32 = 2048 frames stay in registers
+// normalize_columns (src/frontend.rs:225-241).  Input: raw log-mel,
+// frame-major ([T][128] per item, as the log-mel kernel writes it).
+// Output: feature-major ([128][T] per item, the reference's memory order).
+//
+// One workgroup of 8 waves per (item, 32-feature slab).  Loads: the item's
+// frames form rounds of 64; in round j, wave v lane i holds frame
+// 64 j + 8 v + i / 8, features 4 (i % 8) .. + 3 of the slab, so one load
+// instruction reads 8 whole 128-byte frame lines.  Items of up to 64 N frames
+// are read from HBM once and held in registers (N float4s per lane); longer
+// ones are streamed three times.  Stores: chunks of 4 rounds (256 frames)
+// are transposed through LDS, and lane i of wave v writes feature row
+// 4 v + i / 16, frames 4 (i % 16) + 64 s .. + 3, so one store instruction
+// writes 4 rows x 256 contiguous bytes (rows are only 4-byte aligned when T
+// is odd; gfx950 takes unaligned 16-byte stores).
+//
+// Statistics: per-feature sums are reduced across the lanes of a wave by
+// shuffles and across the 8 waves through LDS, always in the same order, so
+// results are deterministic.  The mean and the sum of squared deviations
+// are accumulated in f64, then out = (x - mean) / (sqrt(var) + 1e-5) in f32,
+// var over T - 1 (T == 1 gives NaN, as the reference).  A feature whose
+// values are all equal replays the reference's sequential f32 sums
+// (constant_row_stats).
+constexpr int kNormWaves = 8;
+constexpr int kNormThreads = 64 * kNormWaves;
+constexpr int kNormSlab = 32;                  // features per workgroup
+constexpr int kNormSlabs = kMel / kNormSlab;   // 4
+constexpr int kNormGroup = 8;                  // frames per load instruction
+constexpr int kNormSpan = kNormGroup * kNormWaves;  // frames per round (64)
+constexpr int kNormChunk = 4 * kNormSpan;      // frames per LDS transpose (256)
+constexpr int kNormTStride = kNormChunk + 4;   // LDS row stride (floats), keeps rows 16-byte aligned
 
-// normalize_columns (src/frontend.rs:225-241) for one (item, feature) row per
-// wavefront.  Ordinary rows use exact statistics: the mean and the sum of
-// squared deviations are accumulated in f64, then
-// out = (x - mean) / (sqrt(var) + 1e-5) in f32, with var over T - 1 (T == 1
-// gives NaN, as the reference).  Rows of up to 2048 frames are read from
-// HBM once and held in registers; longer rows are streamed three times.
-__global__ __launch_bounds__(kThreads) void sfe_norm_kernel(const float* __restrict__ raw,
-                                                            const Item* __restrict__ items, int n_items,
-                                                            float* __restrict__ out_f32,
-                                                            uint16_t* __restrict__ out_bf16) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (row >= (int64_t)n_items * kMel) return;
-  const Item it = items[row / kMel];
-  const int m = (int)(row % kMel);
-  const int T = it.T;
-  const int64_t off = it.out_off + (int64_t)m * T;
-  const float* x = raw + off;
-  const float x0 = x[0];
+__device__ __forceinline__ float comp(const float4& v, int c) {
+  return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+}
 
-  float meanf, sdf;
-  if (T <= 64 * kRowRegs) {
-    float v[kRowRegs];
+// Sum over the 8 lanes that share lane % 8 (lanes i, i ^ 8, ..., i ^ 56).
+__device__ __forceinline__ double group_sum(double v) {
+  v += __shfl_xor(v, 8, 64);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// Workgroup reduction of 4 per-lane partials (features 4 q .. 4 q + 3,
+// q = lane % 8) into the totals over the item; every lane gets the totals of
+// its own 4 features.  red holds kNormWaves x 32 doubles.
+__device__ __forceinline__ void slab_sum(double (&v)[4], double* red, int lane, int w) {
 #pragma unroll
-    for (int i = 0; i < kRowRegs; ++i) {
-      const int t = lane + 64 * i;
-      v[i] = t < T ? x[t] : x0;  // padding with x0 keeps the constancy test exact
-    }
-    double s = 0.0;
-    bool eq = true;
+  for (int c = 0; c < 4; ++c) v[c] = group_sum(v[c]);
+  if (lane < 8) {
 #pragma unroll
-    for (int i = 0; i < kRowRegs; ++i) {
-      if (lane + 64 * i < T) s += (double)v[i];
-      eq = eq && (v[i] == x0);
-    }
-    if (__all(eq)) {
-      float r0 = 0.0f, r1 = 0.0f;
-      if (lane == 0) constant_row_stats(x0, T, &r0, &r1);
-      meanf = __shfl(r0, 0, 64);
-      sdf = __shfl(r1, 0, 64);
-    } else {
-      const double mean = wave_sum(s) / (double)T;
-      double q = 0.0;
+    for (int c = 0; c < 4; ++c) red[w * kNormSlab + 4 * lane + c] = v[c];
+  }
+  __syncthreads();
+  const int q = lane & 7;
 #pragma unroll
-      for (int i = 0; i < kRowRegs; ++i) {
-        const double d = (double)v[i] - mean;
-        if (lane + 64 * i < T) q += d * d;
+  for (int c = 0; c < 4; ++c) {
+    double t = 0.0;
+#pragma unroll
+    for (int u = 0; u < kNormWaves; ++u) t += red[u * kNormSlab + 4 * q + c];
+    v[c] = t;
+  }
+  __syncthreads();  // red is reused by the next reduction
+}
+
+// Workgroup AND of 4 per-lane flags, same layout as slab_sum.
+__device__ __forceinline__ void slab_all(bool (&f)[4], int* redi, int lane, int w) {
+  unsigned m = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) m |= (f[c] ? 1u : 0u) << c;
+  m &= __shfl_xor(m, 8, 64);
+  m &= __shfl_xor(m, 16, 64);
+  m &= __shfl_xor(m, 32, 64);
+  if (lane < 8) redi[w * 8 + lane] = (int)m;
+  __syncthreads();
+  unsigned t = 0xfu;
+#pragma unroll
+  for (int u = 0; u < kNormWaves; ++u) t &= (unsigned)redi[u * 8 + (lane & 7)];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) f[c] = (t >> c) & 1u;
+  __syncthreads();
+}
+
+// (x - mean) / sd, correctly rounded, from r = RN(1 / sd): q = RN(d r) is
+// within one ulp of d / sd, and one residual step q + r fma(-sd, q, d)
+// rounds to RN(d / sd) (Markstein's theorem; d and sd are far from overflow
+// and underflow here).  Three VALU operations instead of a full division.
+__device__ __forceinline__ float norm_div(float x, float mean, float sd, float r) {
+  const float d = __fsub_rn(x, mean);
+  const float q = __fmul_rn(d, r);
+  return __fmaf_rn(__fmaf_rn(-sd, q, d), r, q);
+}
+
+// Per-feature (mean, sd, 1/sd) of the slab, published in LDS by the lanes
+// that own each feature (wave 0, lanes 0..7) for the transposed store phase.
+__device__ __forceinline__ void publish_stats(const double (&s)[4], const double (&q)[4], const bool (&cst)[4],
+                                              const float4& x0, int T, int lane, int w, float* st) {
+  if (w == 0 && lane < 8) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float mean, sd;
+      if (cst[c]) {
+        constant_row_stats(comp(x0, c), T, &mean, &sd);
+      } else {
+        mean = (float)(s[c] / (double)T);
+        sd = __fadd_rn(__fsqrt_rn((float)(q[c] / (double)(T - 1))), 1e-5f);
       }
-      const double var = wave_sum(q) / (double)(T - 1);
-      meanf = (float)mean;
-      sdf = __fadd_rn(__fsqrt_rn((float)var), 1e-5f);
+      const int f = 4 * lane + c;
+      st[3 * f] = mean;
+      st[3 * f + 1] = sd;
+      st[3 * f + 2] = __fdiv_rn(1.0f, sd);
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void put4(float* o, float4 y) {
+  typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+  *reinterpret_cast<f4u*>(o) = f4u{y.x, y.y, y.z, y.w};
+}
+__device__ __forceinline__ void put4(uint16_t* o, float4 y) {
+  typedef uint16_t u4u __attribute__((ext_vector_type(4), aligned(2)));
+  *reinterpret_cast<u4u*>(o) = u4u{f32_to_bf16(y.x), f32_to_bf16(y.y), f32_to_bf16(y.z), f32_to_bf16(y.w)};
+}
+__device__ __forceinline__ void put1(float* o, float y) { *o = y; }
+__device__ __forceinline__ void put1(uint16_t* o, float y) { *o = f32_to_bf16(y); }
+
+// Store phase of one chunk: the chunk's frames are in tb[32][kNormTStride]
+// (feature-major); lane i of wave v writes row 4 v + i / 16.
+template <typename O>
+__device__ __forceinline__ void store_chunk(const float* tb, const float* st, int t0, int T, int lane, int w,
+                                            O* __restrict__ ob) {
+  const int r = 4 * w + (lane >> 4);
+  const float mean = st[3 * r], sd = st[3 * r + 1], rc = st[3 * r + 2];
+  O* orow = ob + (size_t)r * T;
+#pragma unroll
+  for (int s = 0; s < kNormChunk / kNormSpan; ++s) {
+    const int k = 4 * (lane & 15) + kNormSpan * s;
+    const float4 x = *reinterpret_cast<const float4*>(tb + r * kNormTStride + k);
+    const float4 y = make_float4(norm_div(x.x, mean, sd, rc), norm_div(x.y, mean, sd, rc),
+                                 norm_div(x.z, mean, sd, rc), norm_div(x.w, mean, sd, rc));
+    const int t = t0 + k;
+    if (t + 3 < T) {
+      put4(orow + t, y);
+    } else {
+      if (t < T) put1(orow + t, y.x);
+      if (t + 1 < T) put1(orow + t + 1, y.y);
+      if (t + 2 < T) put1(orow + t + 2, y.z);
+    }
+  }
+}
+
+// Stage one round's float4 (4 features of frame fr) of the lane into the
+// transpose buffer at column col.
+__device__ __forceinline__ void stage(float* tb, int q, int col, const float4& v) {
+  tb[(4 * q + 0) * kNormTStride + col] = v.x;
+  tb[(4 * q + 1) * kNormTStride + col] = v.y;
+  tb[(4 * q + 2) * kNormTStride + col] = v.z;
+  tb[(4 * q + 3) * kNormTStride + col] = v.w;
+}
+
+template <int N, typename O>
+__global__ __launch_bounds__(kNormThreads) void sfe_norm_kernel(const float* __restrict__ raw,
+                                                                const Item* __restrict__ items, int n_items,
+                                                                O* __restrict__ out) {
+  static_assert(N % 4 == 0, "whole chunks");  // N == 0: always stream
+  __shared__ double red[kNormWaves * kNormSlab];
+  __shared__ int redi[kNormWaves * 8];
+  __shared__ float st[3 * kNormSlab];
+  __shared__ __align__(16) float tb[kNormSlab * kNormTStride];
+  const int item = blockIdx.x / kNormSlabs;
+  if (item >= n_items) return;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int q = lane & 7;
+  const int fr = w * kNormGroup + (lane >> 3);  // frame of this lane in each 64-frame round
+  const int slab = (blockIdx.x % kNormSlabs) * kNormSlab;
+  const Item it = items[item];
+  const int T = it.T;
+  // Uniform bases with 32-bit lane offsets.
+  const float* xb = raw + it.out_off + slab;
+  O* ob = out + it.out_off + (size_t)slab * T;
+  const uint32_t lo = (uint32_t)(fr * kMel + 4 * q);
+  const int nr = fr < T ? (T - 1 - fr) / kNormSpan + 1 : 0;  // rounds holding a frame of this lane
+  const float4 x0 = *reinterpret_cast<const float4*>(xb + 4 * q);
+
+  double s[4] = {0.0, 0.0, 0.0, 0.0}, sq[4] = {0.0, 0.0, 0.0, 0.0};
+  bool eq[4] = {true, true, true, true};
+  if constexpr (N > 0) {
+  if (T <= kNormSpan * N) {
+    float4 v[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      v[j] = x0;  // padding with x0 keeps the constancy test exact
+      if (j < nr) v[j] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
     }
 #pragma unroll
-    for (int i = 0; i < kRowRegs; ++i) {
-      const int t = lane + 64 * i;
-      if (t < T) {
-        const float y = __fdiv_rn(__fsub_rn(v[i], meanf), sdf);
-        if (out_bf16) out_bf16[off + t] = f32_to_bf16(y);
-        else out_f32[off + t] = y;
+    for (int j = 0; j < N; ++j) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (j < nr) s[c] += (double)comp(v[j], c);
+        eq[c] = eq[c] && (comp(v[j], c) == comp(x0, c));
+      }
+    }
+    slab_sum(s, red, lane, w);
+    slab_all(eq, redi, lane, w);
+    double m[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) m[c] = s[c] / (double)T;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const double d = (double)comp(v[j], c) - m[c];
+        if (j < nr) sq[c] += d * d;
+      }
+    }
+    slab_sum(sq, red, lane, w);
+    publish_stats(s, sq, eq, x0, T, lane, w, st);
+    const int chunks = (T + kNormChunk - 1) / kNormChunk;
+#pragma unroll
+    for (int ch = 0; ch < N / 4; ++ch) {
+      if (ch < chunks) {
+#pragma unroll
+        for (int jr = 0; jr < 4; ++jr) stage(tb, q, kNormSpan * jr + fr, v[4 * ch + jr]);
+        __syncthreads();
+        store_chunk(tb, st, kNormChunk * ch, T, lane, w, ob);
+        __syncthreads();
       }
     }
     return;
   }
+  }
 
-  // long rows: three streaming passes
-  double s = 0.0;
-  bool eq = true;
-  for (int t = lane; t < T; t += 64) {
-    const float v = x[t];
-    s += (double)v;
-    eq = eq && (v == x0);
-  }
-  if (__all(eq)) {
-    float r0 = 0.0f, r1 = 0.0f;
-    if (lane == 0) constant_row_stats(x0, T, &r0, &r1);
-    meanf = __shfl(r0, 0, 64);
-    sdf = __shfl(r1, 0, 64);
-  } else {
-    const double mean = wave_sum(s) / (double)T;
-    double q = 0.0;
-    for (int t = lane; t < T; t += 64) {
-      const double d = (double)x[t] - mean;
-      q += d * d;
+  // long items: three streaming passes
+  for (int j = 0; j < nr; ++j) {
+    const float4 e = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s[c] += (double)comp(e, c);
+      eq[c] = eq[c] && (comp(e, c) == comp(x0, c));
     }
-    const double var = wave_sum(q) / (double)(T - 1);
-    meanf = (float)mean;
-    sdf = __fadd_rn(__fsqrt_rn((float)var), 1e-5f);
   }
-  for (int t = lane; t < T; t += 64) {
-    const float y = __fdiv_rn(__fsub_rn(x[t], meanf), sdf);
-    if (out_bf16) out_bf16[off + t] = f32_to_bf16(y);
-    else out_f32[off + t] = y;
+  slab_sum(s, red, lane, w);
+  slab_all(eq, redi, lane, w);
+  double m[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) m[c] = s[c] / (double)T;
+  for (int j = 0; j < nr; ++j) {
+    const float4 e = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const double d = (double)comp(e, c) - m[c];
+      sq[c] += d * d;
+    }
+  }
+  slab_sum(sq, red, lane, w);
+  publish_stats(s, sq, eq, x0, T, lane, w, st);
+  const int chunks = (T + kNormChunk - 1) / kNormChunk;
+  for (int ch = 0; ch < chunks; ++ch) {
+#pragma unroll
+    for (int jr = 0; jr < 4; ++jr) {
+      const int j = 4 * ch + jr;
+      if (j < nr) stage(tb, q, kNormSpan * jr + fr, *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo));
+    }
+    __syncthreads();
+    store_chunk(tb, st, kNormChunk * ch, T, lane, w, ob);
+    __syncthreads();
   }
 }
 
@@ -568,15 +785,26 @@ hipError_t launch_logmel(const float* samples, const Item* items, int n_items, i
   return hipGetLastError();
 }
 
-hipError_t launch_norm(const float* raw, const Item* items, int n_items, void* out, bool out_bf16,
-                       hipStream_t stream) {
-  const int64_t rows = (int64_t)n_items * kMel;
-  const int64_t blocks = (rows + 3) / 4;
-  if (blocks <= 0) return hipSuccess;
-  sfe_norm_kernel<<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
-      raw, items, n_items, out_bf16 ? nullptr : static_cast<float*>(out),
-      out_bf16 ? static_cast<uint16_t*>(out) : nullptr);
+template <typename O>
+hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, O* out, dim3 grid, dim3 block,
+                         hipStream_t stream) {
+  // Registers per lane sized to the longest item (N float4s hold 64 N
+  // frames); items longer than 2048 frames take the streaming path.
+  if (max_T <= kNormSpan * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else if (max_T <= kNormSpan * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else if (max_T <= kNormSpan * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else sfe_norm_kernel<32, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  if (max_T < 0) sfe_norm_kernel<0, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
   return hipGetLastError();
+}
+
+hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, void* out, bool out_bf16,
+                       hipStream_t stream) {
+  const int64_t blocks = (int64_t)n_items * kNormSlabs;
+  if (blocks <= 0) return hipSuccess;
+  const dim3 grid((unsigned)blocks), block(kNormThreads);
+  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, static_cast<uint16_t*>(out), grid, block, stream);
+  return launch_norm_t(raw, items, n_items, max_T, static_cast<float*>(out), grid, block, stream);
 }
 
 }  // namespace sfe
