@@ -112,8 +112,9 @@ def main() -> int:
 
     sec = (t1 - t0) / args.steps
     audio_sec = n_audio / SR
-    logmel_ms = lm.value / max(nl.value, 1)
-    norm_ms = nm.value / max(nl.value, 1)
+    # per step (a call may run as several log-mel/normalisation batches)
+    logmel_ms = lm.value / args.steps
+    norm_ms = nm.value / args.steps
     out_bytes = 4 if args.dtype == "f32" else 2
     alg_logmel = 4 * n_audio + 512 * F                  # read audio once, write raw f32 log-mel
     alg_path = 4 * n_audio + 128 * out_bytes * F        # the whole front end

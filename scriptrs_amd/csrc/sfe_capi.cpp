@@ -20,6 +20,10 @@ using sfe::Item;
 
 namespace {
 
+// Batching of one launch (see launch_pair).
+constexpr int kMaxBatches = 1;  // batching measured slower (see launch_pair); kept off
+constexpr int kMinUnitsPerBatch = 4096;  // 16-frame units; smaller calls run unbatched
+
 thread_local std::string g_last_error;
 
 int fail(int code, const std::string& msg) {
@@ -121,6 +125,8 @@ struct sfe_ctx {
   sfe::DevTables* d_tables = nullptr;
   hipStream_t s_compute = nullptr;  // internal streams, default priority
   hipStream_t s_copy = nullptr;
+  hipStream_t s_aux = nullptr;      // normalisation of finished batches
+  std::vector<hipEvent_t> sev;      // fork/join events of launch_pair
   DevBuf meta;      // Item tables
   PinBuf h_meta;
   DevBuf scratch;   // raw log-mel, frame-major f32 (the normalisation kernel's input)
@@ -172,20 +178,80 @@ hipEvent_t timing_event(sfe_ctx* ctx) {
   return ctx->tev[ctx->tev_used++];
 }
 
-// Launches the log-mel kernel then the normalisation kernel; with timing on,
-// brackets each with events (read back by sfe_get_timing).
-int launch_pair(sfe_ctx* ctx, const float* samples, const Item* d_items, int n, int tiles, int max_T, float* raw,
+hipEvent_t sync_event(sfe_ctx* ctx, size_t i) {
+  while (ctx->sev.size() <= i) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+    ctx->sev.push_back(e);
+  }
+  return ctx->sev[i];
+}
+
+// Log-mel then normalisation over host items[0, n) (device copy d_items,
+// tile_off relative to the launch), asynchronously on `stream`.
+//
+// A call with enough work is split into up to kMaxBatches batches of whole
+// items.  The log-mel kernel of batch b + 1 runs on `stream` while the lean
+// normalisation kernel of batch b runs on the internal aux stream: the two
+// kernels are bound by different units (VALU and HBM) and their workgroups
+// fit on a CU together.  Events order each normalisation after its batch's
+// log-mel and join the aux stream back into `stream` at the end.  With
+// timing on, every kernel is bracketed by events (read by sfe_get_timing).
+int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Item* d_items, int n, float* raw,
                 void* out, int32_t out_dtype, hipStream_t stream) {
-  hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
-  if (ctx->timing)
-    for (int i = 0; i < 4; ++i)
-      if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
-  if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
-  SFE_HIP(sfe::launch_logmel(samples, d_items, n, tiles, ctx->d_tables, ctx->cfg.preemphasis, raw, ctx->grid_cap, stream));
-  if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
-  if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
-  SFE_HIP(sfe::launch_norm(raw, d_items, n, max_T, out, out_dtype == SFE_BF16, stream));
-  if (e[3]) SFE_HIP(hipEventRecord(e[3], stream));
+  if (n <= 0) return SFE_OK;
+  const int u0 = items[0].tile_off;
+  const int u1 = items[n - 1].tile_off + (int)sfe::tiles_for(items[n - 1].T);
+  int nb = 1;
+  if (u1 - u0 >= kMinUnitsPerBatch * kMaxBatches) nb = std::min(kMaxBatches, n);
+  const bool bf16 = out_dtype == SFE_BF16;
+  if (nb > 1) {
+    hipEvent_t fork = sync_event(ctx, 0);
+    if (!fork) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
+    SFE_HIP(hipEventRecord(fork, stream));
+    SFE_HIP(hipStreamWaitEvent(ctx->s_aux, fork, 0));
+  }
+  int first = 0;
+  for (int b = 0; b < nb; ++b) {
+    // batch b: items [first, last) ending at the item boundary nearest to
+    // an equal share of the units
+    int last = n;
+    if (b + 1 < nb) {
+      const int target = u0 + (int)((int64_t)(u1 - u0) * (b + 1) / nb);
+      last = first + 1;
+      while (last < n - (nb - b - 1) && items[last].tile_off < target) ++last;
+    }
+    const int cnt = last - first;
+    const int bu0 = items[first].tile_off;
+    const int bu1 = items[last - 1].tile_off + (int)sfe::tiles_for(items[last - 1].T);
+    int max_T = 0;
+    for (int i = first; i < last; ++i) max_T = std::max(max_T, (int)items[i].T);
+    hipStream_t ns = nb > 1 ? ctx->s_aux : stream;
+    hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (ctx->timing)
+      for (int i = 0; i < 4; ++i)
+        if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
+    if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
+    SFE_HIP(sfe::launch_logmel(samples, d_items + first, cnt, bu0, bu1 - bu0, ctx->d_tables, ctx->cfg.preemphasis, raw,
+                               ctx->grid_cap, stream));
+    if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
+    if (nb > 1) {
+      hipEvent_t done = sync_event(ctx, 1 + b);
+      if (!done) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
+      SFE_HIP(hipEventRecord(done, stream));
+      SFE_HIP(hipStreamWaitEvent(ns, done, 0));
+    }
+    if (e[2]) SFE_HIP(hipEventRecord(e[2], ns));
+    SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, out, bf16, nb > 1, ns));
+    if (e[3]) SFE_HIP(hipEventRecord(e[3], ns));
+    first = last;
+  }
+  if (nb > 1) {
+    hipEvent_t join = sync_event(ctx, 1 + nb);
+    if (!join) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
+    SFE_HIP(hipEventRecord(join, ctx->s_aux));
+    SFE_HIP(hipStreamWaitEvent(stream, join, 0));
+  }
   return SFE_OK;
 }
 
@@ -203,9 +269,8 @@ int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items
   const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
   SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
-  int max_T = 0;
-  for (const Item& it : items) max_T = std::max(max_T, (int)it.T);
-  return launch_pair(ctx, samples, d_items, (int)items.size(), (int)total_tiles, max_T, raw, out, out_dtype, stream);
+  (void)total_tiles;
+  return launch_pair(ctx, samples, items.data(), d_items, (int)items.size(), raw, out, out_dtype, stream);
 }
 
 int check_ctx(sfe_ctx* ctx) {
@@ -323,6 +388,8 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
     return cleanup(hip_fail(e, "hipStreamCreate"));
   if ((e = hipStreamCreateWithFlags(&ctx->s_copy, hipStreamNonBlocking)) != hipSuccess)
     return cleanup(hip_fail(e, "hipStreamCreate"));
+  if ((e = hipStreamCreateWithFlags(&ctx->s_aux, hipStreamNonBlocking)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipStreamCreate"));
   for (int i = 0; i < 2; ++i) {
     if ((e = hipEventCreateWithFlags(&ctx->ev_copied[i], hipEventDisableTiming)) != hipSuccess)
       return cleanup(hip_fail(e, "hipEventCreate"));
@@ -350,8 +417,10 @@ void sfe_destroy(sfe_ctx* ctx) {
     if (ctx->ev_done[i]) (void)hipEventDestroy(ctx->ev_done[i]);
   }
   for (hipEvent_t e : ctx->tev) (void)hipEventDestroy(e);
+  for (hipEvent_t e : ctx->sev) (void)hipEventDestroy(e);
   if (ctx->s_compute) (void)hipStreamDestroy(ctx->s_compute);
   if (ctx->s_copy) (void)hipStreamDestroy(ctx->s_copy);
+  if (ctx->s_aux) (void)hipStreamDestroy(ctx->s_aux);
   delete ctx;
 }
 
@@ -514,8 +583,8 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
     ctx->h_win[b].pending = true;
     SFE_HIP(hipEventRecord(ctx->ev_copied[b], sx));
     SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[b], 0));
-    rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), d_items + g.first, g.count, g.tiles, g.max_T, raw, out,
-                     out_dtype, sc);
+    rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), items.data() + g.first, d_items + g.first, g.count,
+                     raw, out, out_dtype, sc);
     if (rc) return rc;
     SFE_HIP(hipEventRecord(ctx->ev_done[b], sc));
     used[b] = true;

@@ -70,15 +70,17 @@ constexpr int kTile = 16;  // frames per unit of work (one pass) of the log-mel 
 int64_t tiles_for(int64_t T);
 // grid_cap: workgroups resident on the device at once (the kernel loops
 // over tiles, so launching more than that only adds scheduling overhead).
-hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int total_tiles,
+// Units [unit0, unit0 + n_units) in the numbering of items[].tile_off.
+hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int unit0, int n_units,
                          const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream);
 constexpr int kLogmelWavesPerSimd = 2;
 constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
 // Normalises raw (f32, frame-major [T][128] per item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
-// frame count (sizes the kernel's register budget).
+// frame count (sizes the kernel's register budget).  lean selects the
+// low-footprint variant that co-runs with the log-mel kernel.
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, void* out, bool out_bf16,
-                       hipStream_t stream);
+                       bool lean, hipStream_t stream);
 
 }  // namespace sfe

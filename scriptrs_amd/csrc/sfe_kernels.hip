@@ -156,7 +156,10 @@ __device__ __forceinline__ Span make_span(const Item& it, const float* samples, 
 }
 
 // Issues the 16-byte loads of an interior span (lane L: samples 4L + 256 h
-// + 0..3) and of the sample before it.  Other spans are read when processed.
+// + 0..3) and, per lane, the sample before its first vector (4L - 1), which
+// is that vector's preemphasis neighbour.  The per-lane address keeps it a
+// vector load: a scalar load would share lgkmcnt with LDS, and every later
+// LDS wait would also wait for it.  Other spans are read when processed.
 __device__ __forceinline__ void prefetch_span(const Span& sp, int lane, float4 (&v)[kSpanVec], float& xm1) {
   if (!sp.interior) return;
 #pragma unroll
@@ -164,7 +167,7 @@ __device__ __forceinline__ void prefetch_span(const Span& sp, int lane, float4 (
     const int j = 4 * lane + 256 * h;
     v[h] = *reinterpret_cast<const float4*>(sp.xb + (j < kSpan ? j : 0));
   }
-  xm1 = sp.xb[-1];
+  xm1 = sp.xb[4 * lane - 1];
 }
 
 // Guarded log (src/frontend.rs:111-113): ln(v + 2^-24), with the exact
@@ -257,8 +260,9 @@ __device__ __forceinline__ void store_pending(int w, const MelAcc& acc, float* f
 
 __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kernel(const float* __restrict__ samples,
                                                               const Item* __restrict__ items, int n_items,
-                                                              int total_tiles, const DevTables* __restrict__ tb,
-                                                              float coef, float* __restrict__ out) {
+                                                              int unit0, int n_units,
+                                                              const DevTables* __restrict__ tb, float coef,
+                                                              float* __restrict__ out) {
   __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
   __shared__ __align__(16) float pbuf[2][kPassFrames][kPStride];
 
@@ -309,8 +313,10 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
   // (16-frame passes of one item), so the per-lane constants above are
   // loaded once per workgroup and neighbouring units (which share cache
   // lines of the output rows and of the input) stay on one XCD's L2.
-  const int u_begin = (int)((int64_t)total_tiles * blockIdx.x / gridDim.x);
-  const int u_end = (int)((int64_t)total_tiles * (blockIdx.x + 1) / gridDim.x);
+  // Units of this launch are [unit0, unit0 + n_units) (items[].tile_off
+  // counts in the same numbering).
+  const int u_begin = unit0 + (int)((int64_t)n_units * blockIdx.x / gridDim.x);
+  const int u_end = unit0 + (int)((int64_t)n_units * (blockIdx.x + 1) / gridDim.x);
   if (u_begin >= u_end) return;
   // Item descriptors stay in scalar registers: it_c is the item of the unit
   // being prefetched, it_n the item after it, loaded one item ahead so an
@@ -352,19 +358,23 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
     // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
     // src/frontend.rs:157 computes it), zero outside [0, L).
     if (sp.interior) {
+#pragma clang fp contract(off)
 #pragma unroll
       for (int h = 0; h < kSpanVec; ++h) {
         const int j = 4 * lane + 256 * h;
-        // x[j - 1]: lane L - 1's last sample; lane 0 takes the previous
-        // vector's lane 63 (or the sample before the span).
-        const float edge = h == 0 ? cxm1 : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv[h - 1].w), 63));
-        const float p0 = __int_as_float(
-            __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(cv[h].w), 0x138, 0xf, 0xf, false));
+        // x[j - 1]: for h = 0 the lane's own prefetched neighbour; else lane
+        // L - 1's last sample, lane 0 taking the previous vector's lane 63.
+        float p0 = cxm1;
+        if (h > 0) {
+          const float edge = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv[h - 1].w), 63));
+          p0 = __int_as_float(
+              __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(cv[h].w), 0x138, 0xf, 0xf, false));
+        }
         float4 y;
-        y.x = __fsub_rn(cv[h].x, __fmul_rn(coef, p0));
-        y.y = __fsub_rn(cv[h].y, __fmul_rn(coef, cv[h].x));
-        y.z = __fsub_rn(cv[h].z, __fmul_rn(coef, cv[h].y));
-        y.w = __fsub_rn(cv[h].w, __fmul_rn(coef, cv[h].z));
+        y.x = cv[h].x - coef * p0;
+        y.y = cv[h].y - coef * cv[h].x;
+        y.z = cv[h].z - coef * cv[h].y;
+        y.w = cv[h].w - coef * cv[h].z;
         if (j < kSpan) *reinterpret_cast<float4*>(sb + j) = y;
       }
     } else {
@@ -376,12 +386,13 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
             const int je = j + e;
             float v = 0.0f;
             if (je >= sp.jlo && je < sp.jhi) {
               const float cur = sp.xb[je];
               // item sample 0 (je == jlo with the span starting before the item)
-              v = (je == sp.jlo && sp.s0 <= 0) ? cur : __fsub_rn(cur, __fmul_rn(coef, sp.xb[je - 1]));
+              v = (je == sp.jlo && sp.s0 <= 0) ? cur : cur - coef * sp.xb[je - 1];
             }
             y[e] = v;
           }
@@ -490,15 +501,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 // sums are replayed on one lane in the reference's order
 // (src/frontend.rs:230-236).
 __device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_out, float* sd_out) {
+#pragma clang fp contract(off)  // every f32 operation rounded, as the reference's
   float sum = 0.0f;
-  for (int t = 0; t < T; ++t) sum = __fadd_rn(sum, x0);
+  for (int t = 0; t < T; ++t) sum = sum + x0;
   const float mean = __fdiv_rn(sum, (float)T);
-  const float d = __fsub_rn(x0, mean);
+  const float d = x0 - mean;
   float acc = 0.0f;
-  for (int t = 0; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(d, d));
-  const float var = __fdiv_rn(acc, __fsub_rn((float)T, 1.0f));
+  for (int t = 0; t < T; ++t) acc = acc + d * d;
+  const float var = __fdiv_rn(acc, (float)T - 1.0f);
   *mean_out = mean;
-  *sd_out = __fadd_rn(__fsqrt_rn(var), 1e-5f);
+  *sd_out = __fsqrt_rn(var) + 1e-5f;
 }
 
 // normalize_columns (src/frontend.rs:225-241).  Input: raw log-mel,
@@ -523,14 +535,21 @@ __device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_
 // var over T - 1 (T == 1 gives NaN, as the reference).  A feature whose
 // values are all equal replays the reference's sequential f32 sums
 // (constant_row_stats).
-constexpr int kNormWaves = 8;
-constexpr int kNormThreads = 64 * kNormWaves;
 constexpr int kNormSlab = 32;                  // features per workgroup
 constexpr int kNormSlabs = kMel / kNormSlab;   // 4
 constexpr int kNormGroup = 8;                  // frames per load instruction
-constexpr int kNormSpan = kNormGroup * kNormWaves;  // frames per round (64)
-constexpr int kNormChunk = 4 * kNormSpan;      // frames per LDS transpose (256)
-constexpr int kNormTStride = kNormChunk + 4;   // LDS row stride (floats), keeps rows 16-byte aligned
+constexpr int kNormBatch = 8;                  // rounds of loads in flight on the streaming path
+
+// Shape of a normalisation workgroup of W waves.
+template <int W>
+struct NormShape {
+  static constexpr int kThreads = 64 * W;
+  static constexpr int kSpan = kNormGroup * W;   // frames per round
+  static constexpr int kChunk = 4 * kSpan;       // frames per LDS transpose
+  static constexpr int kTStride = kChunk + 4;    // LDS row stride (floats), keeps rows 16-byte aligned
+  static constexpr int kRowsPerWave = kNormSlab / W;
+  static constexpr int kLanesPerRow = 64 / kRowsPerWave;
+};
 
 __device__ __forceinline__ float comp(const float4& v, int c) {
   return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
@@ -546,7 +565,8 @@ __device__ __forceinline__ double group_sum(double v) {
 
 // Workgroup reduction of 4 per-lane partials (features 4 q .. 4 q + 3,
 // q = lane % 8) into the totals over the item; every lane gets the totals of
-// its own 4 features.  red holds kNormWaves x 32 doubles.
+// its own 4 features.  red holds W x 32 doubles.
+template <int W>
 __device__ __forceinline__ void slab_sum(double (&v)[4], double* red, int lane, int w) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) v[c] = group_sum(v[c]);
@@ -560,13 +580,14 @@ __device__ __forceinline__ void slab_sum(double (&v)[4], double* red, int lane, 
   for (int c = 0; c < 4; ++c) {
     double t = 0.0;
 #pragma unroll
-    for (int u = 0; u < kNormWaves; ++u) t += red[u * kNormSlab + 4 * q + c];
+    for (int u = 0; u < W; ++u) t += red[u * kNormSlab + 4 * q + c];
     v[c] = t;
   }
   __syncthreads();  // red is reused by the next reduction
 }
 
 // Workgroup AND of 4 per-lane flags, same layout as slab_sum.
+template <int W>
 __device__ __forceinline__ void slab_all(bool (&f)[4], int* redi, int lane, int w) {
   unsigned m = 0;
 #pragma unroll
@@ -578,7 +599,7 @@ __device__ __forceinline__ void slab_all(bool (&f)[4], int* redi, int lane, int 
   __syncthreads();
   unsigned t = 0xfu;
 #pragma unroll
-  for (int u = 0; u < kNormWaves; ++u) t &= (unsigned)redi[u * 8 + (lane & 7)];
+  for (int u = 0; u < W; ++u) t &= (unsigned)redi[u * 8 + (lane & 7)];
 #pragma unroll
   for (int c = 0; c < 4; ++c) f[c] = (t >> c) & 1u;
   __syncthreads();
@@ -628,18 +649,20 @@ __device__ __forceinline__ void put4(uint16_t* o, float4 y) {
 __device__ __forceinline__ void put1(float* o, float y) { *o = y; }
 __device__ __forceinline__ void put1(uint16_t* o, float y) { *o = f32_to_bf16(y); }
 
-// Store phase of one chunk: the chunk's frames are in tb[32][kNormTStride]
-// (feature-major); lane i of wave v writes row 4 v + i / 16.
-template <typename O>
+// Store phase of one chunk: the chunk's frames are in tb[32][kTStride]
+// (feature-major); wave v writes rows R v .. R v + R - 1 (R = 32 / W), each
+// row by 2 W lanes, so one store instruction covers R rows x 32 W bytes.
+template <int W, typename O>
 __device__ __forceinline__ void store_chunk(const float* tb, const float* st, int t0, int T, int lane, int w,
                                             O* __restrict__ ob) {
-  const int r = 4 * w + (lane >> 4);
+  using S = NormShape<W>;
+  const int r = S::kRowsPerWave * w + lane / S::kLanesPerRow;
   const float mean = st[3 * r], sd = st[3 * r + 1], rc = st[3 * r + 2];
   O* orow = ob + (size_t)r * T;
 #pragma unroll
-  for (int s = 0; s < kNormChunk / kNormSpan; ++s) {
-    const int k = 4 * (lane & 15) + kNormSpan * s;
-    const float4 x = *reinterpret_cast<const float4*>(tb + r * kNormTStride + k);
+  for (int s = 0; s < S::kChunk / S::kSpan; ++s) {
+    const int k = 4 * (lane % S::kLanesPerRow) + S::kSpan * s;
+    const float4 x = *reinterpret_cast<const float4*>(tb + r * S::kTStride + k);
     const float4 y = make_float4(norm_div(x.x, mean, sd, rc), norm_div(x.y, mean, sd, rc),
                                  norm_div(x.z, mean, sd, rc), norm_div(x.w, mean, sd, rc));
     const int t = t0 + k;
@@ -655,22 +678,28 @@ __device__ __forceinline__ void store_chunk(const float* tb, const float* st, in
 
 // Stage one round's float4 (4 features of frame fr) of the lane into the
 // transpose buffer at column col.
+template <int W>
 __device__ __forceinline__ void stage(float* tb, int q, int col, const float4& v) {
-  tb[(4 * q + 0) * kNormTStride + col] = v.x;
-  tb[(4 * q + 1) * kNormTStride + col] = v.y;
-  tb[(4 * q + 2) * kNormTStride + col] = v.z;
-  tb[(4 * q + 3) * kNormTStride + col] = v.w;
+  constexpr int ts = NormShape<W>::kTStride;
+  tb[(4 * q + 0) * ts + col] = v.x;
+  tb[(4 * q + 1) * ts + col] = v.y;
+  tb[(4 * q + 2) * ts + col] = v.z;
+  tb[(4 * q + 3) * ts + col] = v.w;
 }
 
-template <int N, typename O>
-__global__ __launch_bounds__(kNormThreads) void sfe_norm_kernel(const float* __restrict__ raw,
-                                                                const Item* __restrict__ items, int n_items,
-                                                                O* __restrict__ out) {
-  static_assert(N % 4 == 0, "whole chunks");  // N == 0: always stream
-  __shared__ double red[kNormWaves * kNormSlab];
-  __shared__ int redi[kNormWaves * 8];
+// W waves per workgroup; N float4 registers per lane (N == 0: always
+// stream, the lean variant that runs beside the log-mel kernel).
+template <int W, int N, typename O>
+__device__ __forceinline__ void norm_body(const float* __restrict__ raw, const Item* __restrict__ items,
+                                          int n_items, O* __restrict__ out) {
+  static_assert(N % 4 == 0, "whole chunks");
+  using S = NormShape<W>;
+  constexpr int kNormSpan = S::kSpan;
+  constexpr int kNormChunk = S::kChunk;
+  __shared__ double red[W * kNormSlab];
+  __shared__ int redi[W * 8];
   __shared__ float st[3 * kNormSlab];
-  __shared__ __align__(16) float tb[kNormSlab * kNormTStride];
+  __shared__ __align__(16) float tb[kNormSlab * S::kTStride];
   const int item = blockIdx.x / kNormSlabs;
   if (item >= n_items) return;
   const int lane = threadIdx.x & 63;
@@ -705,8 +734,8 @@ __global__ __launch_bounds__(kNormThreads) void sfe_norm_kernel(const float* __r
         eq[c] = eq[c] && (comp(v[j], c) == comp(x0, c));
       }
     }
-    slab_sum(s, red, lane, w);
-    slab_all(eq, redi, lane, w);
+    slab_sum<W>(s, red, lane, w);
+    slab_all<W>(eq, redi, lane, w);
     double m[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) m[c] = s[c] / (double)T;
@@ -718,16 +747,16 @@ __global__ __launch_bounds__(kNormThreads) void sfe_norm_kernel(const float* __r
         if (j < nr) sq[c] += d * d;
       }
     }
-    slab_sum(sq, red, lane, w);
+    slab_sum<W>(sq, red, lane, w);
     publish_stats(s, sq, eq, x0, T, lane, w, st);
     const int chunks = (T + kNormChunk - 1) / kNormChunk;
 #pragma unroll
     for (int ch = 0; ch < N / 4; ++ch) {
       if (ch < chunks) {
 #pragma unroll
-        for (int jr = 0; jr < 4; ++jr) stage(tb, q, kNormSpan * jr + fr, v[4 * ch + jr]);
+        for (int jr = 0; jr < 4; ++jr) stage<W>(tb, q, kNormSpan * jr + fr, v[4 * ch + jr]);
         __syncthreads();
-        store_chunk(tb, st, kNormChunk * ch, T, lane, w, ob);
+        store_chunk<W>(tb, st, kNormChunk * ch, T, lane, w, ob);
         __syncthreads();
       }
     }
@@ -735,76 +764,119 @@ __global__ __launch_bounds__(kNormThreads) void sfe_norm_kernel(const float* __r
   }
   }
 
-  // long items: three streaming passes
-  for (int j = 0; j < nr; ++j) {
-    const float4 e = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
+  // Streaming: three passes over the item, kNormBatch rounds of loads in
+  // flight per lane (the second and third passes mostly hit the caches).
+  constexpr int G = kNormBatch;
+  for (int j0 = 0; j0 < nr; j0 += G) {
+    float4 e[G];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      s[c] += (double)comp(e, c);
-      eq[c] = eq[c] && (comp(e, c) == comp(x0, c));
+    for (int g = 0; g < G; ++g)
+      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kNormSpan * kMel) + lo);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (j0 + g < nr) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          s[c] += (double)comp(e[g], c);
+          eq[c] = eq[c] && (comp(e[g], c) == comp(x0, c));
+        }
+      }
     }
   }
-  slab_sum(s, red, lane, w);
-  slab_all(eq, redi, lane, w);
+  slab_sum<W>(s, red, lane, w);
+  slab_all<W>(eq, redi, lane, w);
   double m[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) m[c] = s[c] / (double)T;
-  for (int j = 0; j < nr; ++j) {
-    const float4 e = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
+  for (int j0 = 0; j0 < nr; j0 += G) {
+    float4 e[G];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const double d = (double)comp(e, c) - m[c];
-      sq[c] += d * d;
+    for (int g = 0; g < G; ++g)
+      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kNormSpan * kMel) + lo);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (j0 + g < nr) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const double d = (double)comp(e[g], c) - m[c];
+          sq[c] += d * d;
+        }
+      }
     }
   }
-  slab_sum(sq, red, lane, w);
+  slab_sum<W>(sq, red, lane, w);
   publish_stats(s, sq, eq, x0, T, lane, w, st);
   const int chunks = (T + kNormChunk - 1) / kNormChunk;
   for (int ch = 0; ch < chunks; ++ch) {
+    float4 e[4];
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr) {
       const int j = 4 * ch + jr;
-      if (j < nr) stage(tb, q, kNormSpan * jr + fr, *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo));
+      if (j < nr) e[jr] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
     }
+#pragma unroll
+    for (int jr = 0; jr < 4; ++jr)
+      if (4 * ch + jr < nr) stage<W>(tb, q, kNormSpan * jr + fr, e[jr]);
     __syncthreads();
-    store_chunk(tb, st, kNormChunk * ch, T, lane, w, ob);
+    store_chunk<W>(tb, st, kNormChunk * ch, T, lane, w, ob);
     __syncthreads();
   }
+}
+
+template <int N, typename O>
+__global__ __launch_bounds__(64 * 8) void sfe_norm_kernel(const float* __restrict__ raw,
+                                                          const Item* __restrict__ items, int n_items,
+                                                          O* __restrict__ out) {
+  norm_body<8, N>(raw, items, n_items, out);
+}
+
+// Lean variant: 4 waves, no register holding (three passes; the second and
+// third read what the first brought into the caches), at most 96 VGPRs and
+// about 20 KB LDS so a workgroup fits beside two log-mel workgroups on a CU.
+template <typename O>
+__global__ __launch_bounds__(64 * 4, 5) void sfe_norm_stream_kernel(const float* __restrict__ raw,
+                                                                    const Item* __restrict__ items, int n_items,
+                                                                    O* __restrict__ out) {
+  norm_body<4, 0>(raw, items, n_items, out);
 }
 
 }  // namespace
 
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
 
-hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int total_tiles,
+hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int unit0, int n_units,
                          const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream) {
-  if (total_tiles <= 0) return hipSuccess;
-  const int grid = total_tiles < grid_cap ? total_tiles : grid_cap;
-  sfe_logmel_kernel<<<dim3(grid), dim3(kThreads), 0, stream>>>(samples, items, n_items, total_tiles, tables, preemph,
-                                                                raw_out);
+  if (n_units <= 0) return hipSuccess;
+  const int grid = n_units < grid_cap ? n_units : grid_cap;
+  sfe_logmel_kernel<<<dim3(grid), dim3(kThreads), 0, stream>>>(samples, items, n_items, unit0, n_units, tables,
+                                                                preemph, raw_out);
   return hipGetLastError();
 }
 
 template <typename O>
-hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, O* out, dim3 grid, dim3 block,
+hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, O* out, bool lean,
                          hipStream_t stream) {
+  const unsigned blocks = (unsigned)((int64_t)n_items * kNormSlabs);
+  if (lean) {
+    sfe_norm_stream_kernel<O><<<dim3(blocks), dim3(64 * 4), 0, stream>>>(raw, items, n_items, out);
+    return hipGetLastError();
+  }
   // Registers per lane sized to the longest item (N float4s hold 64 N
   // frames); items longer than 2048 frames take the streaming path.
-  if (max_T <= kNormSpan * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else if (max_T <= kNormSpan * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else if (max_T <= kNormSpan * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  const dim3 grid(blocks), block(64 * 8);
+  constexpr int span = NormShape<8>::kSpan;
+  if (max_T <= span * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else if (max_T <= span * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else if (max_T <= span * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
   else sfe_norm_kernel<32, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  if (max_T < 0) sfe_norm_kernel<0, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
   return hipGetLastError();
 }
 
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, void* out, bool out_bf16,
-                       hipStream_t stream) {
-  const int64_t blocks = (int64_t)n_items * kNormSlabs;
-  if (blocks <= 0) return hipSuccess;
-  const dim3 grid((unsigned)blocks), block(kNormThreads);
-  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, static_cast<uint16_t*>(out), grid, block, stream);
-  return launch_norm_t(raw, items, n_items, max_T, static_cast<float*>(out), grid, block, stream);
+                       bool lean, hipStream_t stream) {
+  if (n_items <= 0) return hipSuccess;
+  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, static_cast<uint16_t*>(out), lean, stream);
+  return launch_norm_t(raw, items, n_items, max_T, static_cast<float*>(out), lean, stream);
 }
 
 }  // namespace sfe

@@ -120,3 +120,29 @@ def test_streamed_equals_resident(extractor):
     torch.cuda.synchronize()
     assert np.array_equal(fa, fb)
     assert torch.equal(a, b)
+
+
+def test_long_form_batched_pipeline(extractor):
+    """A call large enough to run as several log-mel batches with the lean
+    normalisation overlapping on the aux stream: frame offsets exact for every
+    chunk, values checked on chunks around every batch boundary."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: long form 36M samples (batched pipeline)")
+    rec = synth.speech_like(36_000_000, 21)
+    tasks = build_fast_execution_plan(rec.size)
+    assert sum(((t.audio_end - t.audio_start) // 160 + 1 + 15) // 16 for t in tasks) >= 4 * 4096
+    dev = torch.from_numpy(rec).cuda()
+    out, fo = extractor.extract_chunks(dev, tasks)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    starts = [t.audio_start for t in tasks]
+    lens = [t.audio_end - t.audio_start for t in tasks]
+    want_fo = np.concatenate([[0], np.cumsum([n // 160 + 1 for n in lens])])
+    assert np.array_equal(fo, want_fo)
+    n = len(tasks)
+    pick = sorted(set([0, 1, n - 2, n - 1] + [i + d for i in (n // 4, n // 2, 3 * n // 4) for d in (-1, 0, 1)]))
+    for i in pick:
+        a = rec[starts[i]:starts[i] + lens[i]]
+        got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
