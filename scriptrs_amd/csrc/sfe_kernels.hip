@@ -517,89 +517,93 @@ __device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_
 // frame-major ([T][128] per item, as the log-mel kernel writes it).
 // Output: feature-major ([128][T] per item, the reference's memory order).
 //
-// One workgroup of 8 waves per (item, 32-feature slab).  Loads: the item's
-// frames form rounds of 64; in round j, wave v lane i holds frame
-// 64 j + 8 v + i / 8, features 4 (i % 8) .. + 3 of the slab, so one load
-// instruction reads 8 whole 128-byte frame lines.  Items of up to 64 N frames
-// are read from HBM once and held in registers (N float4s per lane); longer
-// ones are streamed three times.  Stores: chunks of 4 rounds (256 frames)
-// are transposed through LDS, and lane i of wave v writes feature row
-// 4 v + i / 16, frames 4 (i % 16) + 64 s .. + 3, so one store instruction
-// writes 4 rows x 256 contiguous bytes (rows are only 4-byte aligned when T
-// is odd; gfx950 takes unaligned 16-byte stores).
+// One workgroup of W waves per (item, slab of F features).  Loads: in round
+// j, lane i of wave v holds frame j R + v (256 / F) + i / (F / 4) (R frames
+// per round), features 4 (i % (F / 4)) .. + 3 of the slab, as one float4.
+// Items of up to R N frames are read from HBM once and held in registers (N
+// float4s per lane); longer ones are streamed three times.  Stores: chunks
+// of 4 rounds are transposed through LDS and each lane writes 4 consecutive
+// frames of one feature row, so a store instruction covers F / W rows of
+// contiguous bytes (rows are only 4-byte aligned when T is odd; gfx950 takes
+// unaligned 16-byte stores).
 //
-// Statistics: per-feature sums are reduced across the lanes of a wave by
-// shuffles and across the 8 waves through LDS, always in the same order, so
-// results are deterministic.  The mean and the sum of squared deviations
-// are accumulated in f64, then out = (x - mean) / (sqrt(var) + 1e-5) in f32,
-// var over T - 1 (T == 1 gives NaN, as the reference).  A feature whose
+// Statistics: per-lane sums of (x - x0) (x0 the feature's first value) in
+// f32 over at most kNormFlush values, accumulated in f64, then reduced
+// across lanes by shuffles and across waves through LDS, always in the same
+// order, so results are deterministic; the sum of squared deviations from
+// the f32 mean likewise.  Then out = (x - mean) / (sqrt(var) + 1e-5) in
+// f32, var over T - 1 (T == 1 gives NaN, as the reference).  A feature whose
 // values are all equal replays the reference's sequential f32 sums
 // (constant_row_stats).
-constexpr int kNormSlab = 32;                  // features per workgroup
-constexpr int kNormSlabs = kMel / kNormSlab;   // 4
-constexpr int kNormGroup = 8;                  // frames per load instruction
 constexpr int kNormBatch = 8;                  // rounds of loads in flight on the streaming path
+constexpr int kNormFlush = 8;                  // f32 partial sums span at most this many values
 
-// Shape of a normalisation workgroup of W waves.
-template <int W>
+// Shape of a normalisation workgroup: W waves, a slab of F features.
+template <int W, int F>
 struct NormShape {
+  static_assert(F == 16 || F == 32, "slab of 16 or 32 features");
   static constexpr int kThreads = 64 * W;
-  static constexpr int kSpan = kNormGroup * W;   // frames per round
-  static constexpr int kChunk = 4 * kSpan;       // frames per LDS transpose
-  static constexpr int kTStride = kChunk + 4;    // LDS row stride (floats), keeps rows 16-byte aligned
-  static constexpr int kRowsPerWave = kNormSlab / W;
-  static constexpr int kLanesPerRow = 64 / kRowsPerWave;
+  static constexpr int kLanesPerFrame = F / 4;            // float4 per lane
+  static constexpr int kGroup = 64 / kLanesPerFrame;      // frames per load instruction
+  static constexpr int kSpan = kGroup * W;                // frames per round
+  static constexpr int kChunk = 4 * kSpan;                // frames per LDS transpose
+  static constexpr int kTStride = kChunk + 4;             // LDS row stride (floats), rows 16-byte aligned
+  static constexpr int kRowsPerWave = F / W;
+  static constexpr int kLanesPerRow = 64 / kRowsPerWave;  // each writes 4 frames per store
+  static constexpr int kSlabs = kMel / F;
+  static_assert(4 * kLanesPerRow == kSpan, "a store instruction covers one round of a row");
 };
 
 __device__ __forceinline__ float comp(const float4& v, int c) {
   return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
 }
 
-// Sum over the 8 lanes that share lane % 8 (lanes i, i ^ 8, ..., i ^ 56).
+// Sum over the lanes that hold the same features (lane % L equal).
+template <int L>
 __device__ __forceinline__ double group_sum(double v) {
-  v += __shfl_xor(v, 8, 64);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
+#pragma unroll
+  for (int off = L; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
 
 // Workgroup reduction of 4 per-lane partials (features 4 q .. 4 q + 3,
-// q = lane % 8) into the totals over the item; every lane gets the totals of
-// its own 4 features.  red holds W x 32 doubles.
-template <int W>
+// q = lane % (F / 4)) into the totals over the item; every lane gets the
+// totals of its own 4 features.  red holds W x F doubles.
+template <int W, int F>
 __device__ __forceinline__ void slab_sum(double (&v)[4], double* red, int lane, int w) {
+  constexpr int L = F / 4;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = group_sum(v[c]);
-  if (lane < 8) {
+  for (int c = 0; c < 4; ++c) v[c] = group_sum<L>(v[c]);
+  if (lane < L) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) red[w * kNormSlab + 4 * lane + c] = v[c];
+    for (int c = 0; c < 4; ++c) red[w * F + 4 * lane + c] = v[c];
   }
   __syncthreads();
-  const int q = lane & 7;
+  const int q = lane % L;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     double t = 0.0;
 #pragma unroll
-    for (int u = 0; u < W; ++u) t += red[u * kNormSlab + 4 * q + c];
+    for (int u = 0; u < W; ++u) t += red[u * F + 4 * q + c];
     v[c] = t;
   }
   __syncthreads();  // red is reused by the next reduction
 }
 
 // Workgroup AND of 4 per-lane flags, same layout as slab_sum.
-template <int W>
+template <int W, int F>
 __device__ __forceinline__ void slab_all(bool (&f)[4], int* redi, int lane, int w) {
+  constexpr int L = F / 4;
   unsigned m = 0;
 #pragma unroll
   for (int c = 0; c < 4; ++c) m |= (f[c] ? 1u : 0u) << c;
-  m &= __shfl_xor(m, 8, 64);
-  m &= __shfl_xor(m, 16, 64);
-  m &= __shfl_xor(m, 32, 64);
-  if (lane < 8) redi[w * 8 + lane] = (int)m;
+#pragma unroll
+  for (int off = L; off < 64; off <<= 1) m &= __shfl_xor(m, off, 64);
+  if (lane < L) redi[w * L + lane] = (int)m;
   __syncthreads();
   unsigned t = 0xfu;
 #pragma unroll
-  for (int u = 0; u < W; ++u) t &= (unsigned)redi[u * 8 + (lane & 7)];
+  for (int u = 0; u < W; ++u) t &= (unsigned)redi[u * L + lane % L];
 #pragma unroll
   for (int c = 0; c < 4; ++c) f[c] = (t >> c) & 1u;
   __syncthreads();
@@ -615,18 +619,20 @@ __device__ __forceinline__ float norm_div(float x, float mean, float sd, float r
   return __fmaf_rn(__fmaf_rn(-sd, q, d), r, q);
 }
 
+// s holds sums of (x - x0), q sums of squared deviations from the f32 mean.
 // Per-feature (mean, sd, 1/sd) of the slab, published in LDS by the lanes
-// that own each feature (wave 0, lanes 0..7) for the transposed store phase.
+// that own each feature (wave 0, lanes 0 .. F / 4 - 1) for the store phase.
+template <int F>
 __device__ __forceinline__ void publish_stats(const double (&s)[4], const double (&q)[4], const bool (&cst)[4],
                                               const float4& x0, int T, int lane, int w, float* st) {
-  if (w == 0 && lane < 8) {
+  if (w == 0 && lane < F / 4) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float mean, sd;
       if (cst[c]) {
         constant_row_stats(comp(x0, c), T, &mean, &sd);
       } else {
-        mean = (float)(s[c] / (double)T);
+        mean = (float)((double)comp(x0, c) + s[c] / (double)T);
         sd = __fadd_rn(__fsqrt_rn((float)(q[c] / (double)(T - 1))), 1e-5f);
       }
       const int f = 4 * lane + c;
@@ -649,13 +655,12 @@ __device__ __forceinline__ void put4(uint16_t* o, float4 y) {
 __device__ __forceinline__ void put1(float* o, float y) { *o = y; }
 __device__ __forceinline__ void put1(uint16_t* o, float y) { *o = f32_to_bf16(y); }
 
-// Store phase of one chunk: the chunk's frames are in tb[32][kTStride]
-// (feature-major); wave v writes rows R v .. R v + R - 1 (R = 32 / W), each
-// row by 2 W lanes, so one store instruction covers R rows x 32 W bytes.
-template <int W, typename O>
+// Store phase of one chunk: its frames are in tb[F][kTStride]
+// (feature-major); wave v writes rows R v .. R v + R - 1 (R = F / W).
+template <int W, int F, typename O>
 __device__ __forceinline__ void store_chunk(const float* tb, const float* st, int t0, int T, int lane, int w,
                                             O* __restrict__ ob) {
-  using S = NormShape<W>;
+  using S = NormShape<W, F>;
   const int r = S::kRowsPerWave * w + lane / S::kLanesPerRow;
   const float mean = st[3 * r], sd = st[3 * r + 1], rc = st[3 * r + 2];
   O* orow = ob + (size_t)r * T;
@@ -676,92 +681,100 @@ __device__ __forceinline__ void store_chunk(const float* tb, const float* st, in
   }
 }
 
-// Stage one round's float4 (4 features of frame fr) of the lane into the
+// Stage one round's float4 (4 features of one frame) of the lane into the
 // transpose buffer at column col.
-template <int W>
+template <int W, int F>
 __device__ __forceinline__ void stage(float* tb, int q, int col, const float4& v) {
-  constexpr int ts = NormShape<W>::kTStride;
+  constexpr int ts = NormShape<W, F>::kTStride;
   tb[(4 * q + 0) * ts + col] = v.x;
   tb[(4 * q + 1) * ts + col] = v.y;
   tb[(4 * q + 2) * ts + col] = v.z;
   tb[(4 * q + 3) * ts + col] = v.w;
 }
 
-// W waves per workgroup; N float4 registers per lane (N == 0: always
-// stream, the lean variant that runs beside the log-mel kernel).
-template <int W, int N, typename O>
+// W waves, slab of F features, N float4 registers per lane (N == 0: always
+// stream, the lean variant).  `work` is the (item, slab) index.
+template <int W, int F, int N, typename O>
 __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const Item* __restrict__ items,
-                                          int n_items, O* __restrict__ out) {
+                                          int n_items, int work, O* __restrict__ out) {
   static_assert(N % 4 == 0, "whole chunks");
-  using S = NormShape<W>;
-  constexpr int kNormSpan = S::kSpan;
-  constexpr int kNormChunk = S::kChunk;
-  __shared__ double red[W * kNormSlab];
-  __shared__ int redi[W * 8];
-  __shared__ float st[3 * kNormSlab];
-  __shared__ __align__(16) float tb[kNormSlab * S::kTStride];
-  const int item = blockIdx.x / kNormSlabs;
+  using S = NormShape<W, F>;
+  constexpr int kSpan = S::kSpan;
+  constexpr int kChunk = S::kChunk;
+  __shared__ double red[W * F];
+  __shared__ int redi[W * (F / 4)];
+  __shared__ float st[3 * F];
+  __shared__ __align__(16) float tb[F * S::kTStride];
+  const int item = work / S::kSlabs;
   if (item >= n_items) return;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  const int q = lane & 7;
-  const int fr = w * kNormGroup + (lane >> 3);  // frame of this lane in each 64-frame round
-  const int slab = (blockIdx.x % kNormSlabs) * kNormSlab;
+  const int q = lane % S::kLanesPerFrame;
+  const int fr = w * S::kGroup + lane / S::kLanesPerFrame;  // frame of this lane in each round
+  const int slab = (work % S::kSlabs) * F;
   const Item it = items[item];
   const int T = it.T;
   // Uniform bases with 32-bit lane offsets.
   const float* xb = raw + it.out_off + slab;
   O* ob = out + it.out_off + (size_t)slab * T;
   const uint32_t lo = (uint32_t)(fr * kMel + 4 * q);
-  const int nr = fr < T ? (T - 1 - fr) / kNormSpan + 1 : 0;  // rounds holding a frame of this lane
+  const int nr = fr < T ? (T - 1 - fr) / kSpan + 1 : 0;  // rounds holding a frame of this lane
   const float4 x0 = *reinterpret_cast<const float4*>(xb + 4 * q);
 
   double s[4] = {0.0, 0.0, 0.0, 0.0}, sq[4] = {0.0, 0.0, 0.0, 0.0};
   bool eq[4] = {true, true, true, true};
   if constexpr (N > 0) {
-  if (T <= kNormSpan * N) {
-    float4 v[N];
+    if (T <= kSpan * N) {
+      float4 v[N];
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-      v[j] = x0;  // padding with x0 keeps the constancy test exact
-      if (j < nr) v[j] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
-    }
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
+      for (int j = 0; j < N; ++j) {
+        v[j] = x0;  // padding with x0 keeps the constancy test exact
+        if (j < nr) v[j] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo);
+      }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        if (j < nr) s[c] += (double)comp(v[j], c);
-        eq[c] = eq[c] && (comp(v[j], c) == comp(x0, c));
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+          if (j < nr) a += comp(v[j], c) - comp(x0, c);
+          eq[c] = eq[c] && (comp(v[j], c) == comp(x0, c));
+          if ((j + 1) % kNormFlush == 0 || j + 1 == N) {
+            s[c] += (double)a;
+            a = 0.0f;
+          }
+        }
       }
-    }
-    slab_sum<W>(s, red, lane, w);
-    slab_all<W>(eq, redi, lane, w);
-    double m[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) m[c] = s[c] / (double)T;
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
+      slab_sum<W, F>(s, red, lane, w);
+      slab_all<W, F>(eq, redi, lane, w);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const double d = (double)comp(v[j], c) - m[c];
-        if (j < nr) sq[c] += d * d;
-      }
-    }
-    slab_sum<W>(sq, red, lane, w);
-    publish_stats(s, sq, eq, x0, T, lane, w, st);
-    const int chunks = (T + kNormChunk - 1) / kNormChunk;
+        const float m = (float)((double)comp(x0, c) + s[c] / (double)T);
+        float a = 0.0f;
 #pragma unroll
-    for (int ch = 0; ch < N / 4; ++ch) {
-      if (ch < chunks) {
-#pragma unroll
-        for (int jr = 0; jr < 4; ++jr) stage<W>(tb, q, kNormSpan * jr + fr, v[4 * ch + jr]);
-        __syncthreads();
-        store_chunk<W>(tb, st, kNormChunk * ch, T, lane, w, ob);
-        __syncthreads();
+        for (int j = 0; j < N; ++j) {
+          const float d = comp(v[j], c) - m;
+          if (j < nr) a += d * d;
+          if ((j + 1) % kNormFlush == 0 || j + 1 == N) {
+            sq[c] += (double)a;
+            a = 0.0f;
+          }
+        }
       }
+      slab_sum<W, F>(sq, red, lane, w);
+      publish_stats<F>(s, sq, eq, x0, T, lane, w, st);
+      const int chunks = (T + kChunk - 1) / kChunk;
+#pragma unroll
+      for (int ch = 0; ch < N / 4; ++ch) {
+        if (ch < chunks) {
+#pragma unroll
+          for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, v[4 * ch + jr]);
+          __syncthreads();
+          store_chunk<W, F>(tb, st, kChunk * ch, T, lane, w, ob);
+          __syncthreads();
+        }
+      }
+      return;
     }
-    return;
-  }
   }
 
   // Streaming: three passes over the item, kNormBatch rounds of loads in
@@ -771,73 +784,87 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     float4 e[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
-      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kNormSpan * kMel) + lo);
+      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (j0 + g < nr) {
+    for (int c = 0; c < 4; ++c) {
+      float a = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          s[c] += (double)comp(e[g], c);
+      for (int g = 0; g < G; ++g) {
+        if (j0 + g < nr) {
+          a += comp(e[g], c) - comp(x0, c);
           eq[c] = eq[c] && (comp(e[g], c) == comp(x0, c));
         }
       }
+      s[c] += (double)a;
     }
   }
-  slab_sum<W>(s, red, lane, w);
-  slab_all<W>(eq, redi, lane, w);
-  double m[4];
+  slab_sum<W, F>(s, red, lane, w);
+  slab_all<W, F>(eq, redi, lane, w);
+  float m[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) m[c] = s[c] / (double)T;
+  for (int c = 0; c < 4; ++c) m[c] = (float)((double)comp(x0, c) + s[c] / (double)T);
   for (int j0 = 0; j0 < nr; j0 += G) {
     float4 e[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
-      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kNormSpan * kMel) + lo);
+      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (j0 + g < nr) {
+    for (int c = 0; c < 4; ++c) {
+      float a = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const double d = (double)comp(e[g], c) - m[c];
-          sq[c] += d * d;
-        }
+      for (int g = 0; g < G; ++g) {
+        const float d = comp(e[g], c) - m[c];
+        if (j0 + g < nr) a += d * d;
       }
+      sq[c] += (double)a;
     }
   }
-  slab_sum<W>(sq, red, lane, w);
-  publish_stats(s, sq, eq, x0, T, lane, w, st);
-  const int chunks = (T + kNormChunk - 1) / kNormChunk;
+  slab_sum<W, F>(sq, red, lane, w);
+  publish_stats<F>(s, sq, eq, x0, T, lane, w, st);
+  const int chunks = (T + kChunk - 1) / kChunk;
   for (int ch = 0; ch < chunks; ++ch) {
     float4 e[4];
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr) {
       const int j = 4 * ch + jr;
-      if (j < nr) e[jr] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kNormSpan * kMel) + lo);
+      if (j < nr) e[jr] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo);
     }
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr)
-      if (4 * ch + jr < nr) stage<W>(tb, q, kNormSpan * jr + fr, e[jr]);
+      if (4 * ch + jr < nr) stage<W, F>(tb, q, kSpan * jr + fr, e[jr]);
     __syncthreads();
-    store_chunk<W>(tb, st, kNormChunk * ch, T, lane, w, ob);
+    store_chunk<W, F>(tb, st, kChunk * ch, T, lane, w, ob);
     __syncthreads();
   }
 }
 
-template <int N, typename O>
-__global__ __launch_bounds__(64 * 8) void sfe_norm_kernel(const float* __restrict__ raw,
-                                                          const Item* __restrict__ items, int n_items,
-                                                          O* __restrict__ out) {
-  norm_body<8, N>(raw, items, n_items, out);
+// Workgroups of kNormMainWaves waves over 16-feature slabs, two per CU.
+// The two slabs of one 128-byte frame line go to workgroups 8 apart, which
+// the dispatcher places on the same XCD (round-robin over the 8 XCDs), so
+// the second half-line read hits that XCD's L2.
+constexpr int kNormMainWaves = 4;
+constexpr int kNormMainSlab = 16;
+
+__device__ __forceinline__ int xcd_pair_work(int b) {
+  // b = 16 k + 8 h + x  ->  work 16 k + 2 x + h
+  return (b & ~15) + 2 * (b & 7) + ((b >> 3) & 1);
 }
 
-// Lean variant: 4 waves, no register holding (three passes; the second and
-// third read what the first brought into the caches), at most 96 VGPRs and
-// about 20 KB LDS so a workgroup fits beside two log-mel workgroups on a CU.
+template <int N, typename O>
+__global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const float* __restrict__ raw,
+                                                                       const Item* __restrict__ items, int n_items,
+                                                                       O* __restrict__ out) {
+  norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, xcd_pair_work(blockIdx.x), out);
+}
+
+// Lean variant: 4 waves over 32-feature slabs, no register holding (three
+// passes), at most 96 VGPRs and about 20 KB LDS so a workgroup fits beside
+// two log-mel workgroups on a CU.
 template <typename O>
 __global__ __launch_bounds__(64 * 4, 5) void sfe_norm_stream_kernel(const float* __restrict__ raw,
                                                                     const Item* __restrict__ items, int n_items,
                                                                     O* __restrict__ out) {
-  norm_body<4, 0>(raw, items, n_items, out);
+  norm_body<4, 32, 0>(raw, items, n_items, blockIdx.x, out);
 }
 
 }  // namespace
@@ -856,18 +883,20 @@ hipError_t launch_logmel(const float* samples, const Item* items, int n_items, i
 template <typename O>
 hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, O* out, bool lean,
                          hipStream_t stream) {
-  const unsigned blocks = (unsigned)((int64_t)n_items * kNormSlabs);
   if (lean) {
+    const unsigned blocks = (unsigned)((int64_t)n_items * NormShape<4, 32>::kSlabs);
     sfe_norm_stream_kernel<O><<<dim3(blocks), dim3(64 * 4), 0, stream>>>(raw, items, n_items, out);
     return hipGetLastError();
   }
-  // Registers per lane sized to the longest item (N float4s hold 64 N
-  // frames); items longer than 2048 frames take the streaming path.
-  const dim3 grid(blocks), block(64 * 8);
-  constexpr int span = NormShape<8>::kSpan;
-  if (max_T <= span * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else if (max_T <= span * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else if (max_T <= span * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  using S = NormShape<kNormMainWaves, kNormMainSlab>;
+  // whole groups of 16 workgroups (xcd_pair_work); the extra ones exit
+  const unsigned blocks = (unsigned)(((int64_t)n_items * S::kSlabs + 15) / 16 * 16);
+  const dim3 grid(blocks), block(S::kThreads);
+  // Registers per lane sized to the longest item (N float4s hold kSpan N
+  // frames); longer items take the streaming path.
+  if (max_T <= S::kSpan * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else if (max_T <= S::kSpan * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  else if (max_T <= S::kSpan * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
   else sfe_norm_kernel<32, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
   return hipGetLastError();
 }
