@@ -120,6 +120,18 @@ def main() -> int:
     alg_path = 4 * n_audio + 128 * out_bytes * F        # the whole front end
     achieved = alg_logmel / (logmel_ms * 1e-3) / 1e9
 
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "sfe_logmel_longform_1h_traffic.json")
+    if args.workload == "config3" and os.path.exists(tfile):
+        # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+        # (scaled by a plain copy's counters); only valid for the kernel
+        # source those runs measured.
+        import hashlib
+        t = json.load(open(tfile))
+        src = open(os.path.join(ROOT, t["kernel_source"]), "rb").read()
+        if hashlib.sha256(src).hexdigest() == t["kernel_source_sha256"]:
+            traffic = t["traffic_bytes"]
+
     result = {
         "metric": "audio-sec featurized/sec (RTFx) + achieved HBM GB/s vs peak, 1 MI355X",
         "value": audio_sec / sec,
@@ -136,7 +148,7 @@ def main() -> int:
         "config": {"workload": f"{args.workload}: {desc}", "n_audio_samples": n_audio, "chunks": len(tasks),
                    "frames_out": F, "out_dtype": args.dtype},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "sfe_logmel_kernel",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "sfe_logmel_kernel",
                      "kernel_ms": logmel_ms, "alg_bytes": alg_logmel},
         "kernels_ms": {"sfe_logmel_kernel": logmel_ms, "sfe_norm_kernel": norm_ms},
         "path_gbps": alg_path / sec / 1e9,
@@ -156,8 +168,11 @@ def main() -> int:
         result["cpu_baseline"] = {"value": audio_sec / (c1 - c0), "unit": "audio-s/s", "cores": 4, "kind": "port",
                                   "sample": f"the whole {args.workload} workload ({len(tasks)} items), "
                                             "oracle/sfe_oracle.c with 4 worker threads, 1 run"}
-        result["parity"] = {"max_abs_err": float(np.nanmax(err)), "within_tol": bool(np.all((err <= tol) | np.isnan(want)))
-                            if args.dtype == "f32" else None}
+        # A summary only: the parity gate is tests/test_gpu_parity.py, whose
+        # bound also admits the f32 FFT noise of bins near the 2^-24 guard.
+        ok = (err <= tol) | np.isnan(want)
+        result["parity"] = {"max_abs_err_vs_oracle": float(np.nanmax(err)),
+                            "frac_within_1e-4_abs_1e-3_rel": float(ok.mean())}
     print(json.dumps(result), flush=True)
     ext.close()
     return 0

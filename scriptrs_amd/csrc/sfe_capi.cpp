@@ -6,7 +6,6 @@
 // in the HIP kernels of sfe_kernels.hip; there is no CPU compute path.
 #include <hip/hip_runtime.h>
 #include <stdio.h>
-#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -243,7 +242,7 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Ite
       SFE_HIP(hipStreamWaitEvent(ns, done, 0));
     }
     if (e[2]) SFE_HIP(hipEventRecord(e[2], ns));
-    SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, out, bf16, nb > 1 || getenv("SFE_LEAN") != nullptr, ns));
+    SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, out, bf16, nb > 1, ns));
     if (e[3]) SFE_HIP(hipEventRecord(e[3], ns));
     first = last;
   }
