@@ -38,7 +38,7 @@ static_assert(wave_steps(0) <= kMaxSteps && wave_steps(1) <= kMaxSteps && wave_s
 
 // One featurized item: a clip or a long-form chunk task.  samples[start,
 // start+len) is featurized into out[out_off + m*T + t] (raw log-mel in
-// scratch at raw[out_off + t*128 + m]).
+// scratch at raw[out_off + t*128 + m], as log2; times ln 2 is the log-mel).
 struct Item {
   int64_t start;
   int64_t len;
@@ -75,7 +75,7 @@ hipError_t launch_logmel(const float* samples, const Item* items, int n_items, i
                          const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream);
 constexpr int kLogmelWavesPerSimd = 2;
 constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
-// Normalises raw (f32, frame-major [T][128] per item) per (item, feature)
+// Normalises raw (f32 log2 values, frame-major [T][128] per item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
 // frame count (sizes the kernel's register budget).  lean selects the

@@ -6,7 +6,8 @@
 //   preemphasis restarted at the item start -> 256-zero padding ->
 //   400-tap left-aligned Hann window -> 512-point real FFT -> |X|^2 ->
 //   128x257 Slaney mel contraction -> ln(x + 2^-24)
-// and writes the raw log-mel frame-major ([T][128] per item) to scratch.
+// and writes the raw log-mel frame-major ([T][128] per item) to scratch, in
+// base 2 (the normalisation kernel multiplies by ln 2 as it loads).
 // sfe_norm_kernel then applies normalize_columns (src/frontend.rs:225-241)
 // per (item, feature) and writes the reference's feature-major layout
 // ([128][T] per item).
@@ -31,9 +32,6 @@ constexpr int kThreads = 256;
 constexpr int kXStride = 17;                         // transpose row stride (complex)
 constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
 constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
-// ln(2^-24) rounded to f32, the value the reference's f32 ln returns for a
-// mel value of exactly zero.
-constexpr float kLnGuard = -16.635532333438687f;
 constexpr float kLn2 = 0.69314718055994531f;
 
 struct __align__(8) cf {
@@ -170,11 +168,19 @@ __device__ __forceinline__ void prefetch_span(const Span& sp, int lane, float4 (
   xm1 = sp.xb[4 * lane - 1];
 }
 
-// Guarded log (src/frontend.rs:111-113): ln(v + 2^-24), with the exact
-// f32 value of ln(2^-24) when the mel value adds nothing to the guard.
-__device__ __forceinline__ float guarded_log(float v) {
-  const float u = v + kGuard;
-  return (u == kGuard) ? kLnGuard : __log2f(u) * kLn2;
+// Guarded log (src/frontend.rs:111-113) in base 2: log2(v + 2^-24).  The
+// log-mel value is this times ln 2, rounded to f32, which the
+// normalisation kernel applies as it loads the raw values (ln2_scale), so
+// the VALU-bound log-mel kernel does one operation less per value.
+// A mel value that adds nothing to the guard gives log2(2^-24) = -24
+// exactly, and -24 * f32(ln 2) rounds to f32(ln 2^-24), the reference's
+// value for digital silence.
+__device__ __forceinline__ float guarded_log2(float v) { return __log2f(v + kGuard); }
+
+// Raw value loaded by the normalisation kernel: RN(log2 * ln 2).
+__device__ __forceinline__ float4 ln2_scale(float4 v) {
+#pragma clang fp contract(off)  // rounded on its own, never fused into a later add
+  return make_float4(v.x * kLn2, v.y * kLn2, v.z * kLn2, v.w * kLn2);
 }
 
 // Independent accumulator chains per block: a long block's steps alternate
@@ -236,7 +242,7 @@ __device__ __forceinline__ void mel_mfma(const float (&av)[kMaxSteps], const int
 // The 4 waves of a pass together cover whole 512-byte frame rows.
 __device__ __forceinline__ void store_block(const f32x4& v, int b, float* frame_row, int kk) {
   *reinterpret_cast<float4*>(frame_row + 16 * b + 4 * kk) =
-      make_float4(guarded_log(v[0]), guarded_log(v[1]), guarded_log(v[2]), guarded_log(v[3]));
+      make_float4(guarded_log2(v[0]), guarded_log2(v[1]), guarded_log2(v[2]), guarded_log2(v[3]));
 }
 
 template <int W>
@@ -719,7 +725,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   O* ob = out + it.out_off + (size_t)slab * T;
   const uint32_t lo = (uint32_t)(fr * kMel + 4 * q);
   const int nr = fr < T ? (T - 1 - fr) / kSpan + 1 : 0;  // rounds holding a frame of this lane
-  const float4 x0 = *reinterpret_cast<const float4*>(xb + 4 * q);
+  const float4 x0 = ln2_scale(*reinterpret_cast<const float4*>(xb + 4 * q));
 
   double s[4] = {0.0, 0.0, 0.0, 0.0}, sq[4] = {0.0, 0.0, 0.0, 0.0};
   bool eq[4] = {true, true, true, true};
@@ -729,7 +735,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
       for (int j = 0; j < N; ++j) {
         v[j] = x0;  // padding with x0 keeps the constancy test exact
-        if (j < nr) v[j] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo);
+        if (j < nr) v[j] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -784,7 +790,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     float4 e[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
-      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo);
+      if (j0 + g < nr) e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo));
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float a = 0.0f;
@@ -807,7 +813,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     float4 e[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
-      if (j0 + g < nr) e[g] = *reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo);
+      if (j0 + g < nr) e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo));
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float a = 0.0f;
@@ -827,7 +833,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr) {
       const int j = 4 * ch + jr;
-      if (j < nr) e[jr] = *reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo);
+      if (j < nr) e[jr] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
     }
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr)
