@@ -156,6 +156,19 @@ int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets
 int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
                        int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream);
 
+/* Encoder-ready long-form extraction: as sfe_extract_chunks, but chunk i is
+ * written in the encoder input layout that EncoderInputBuffer::
+ * copy_from_features builds on the host (src/model.rs:241-278):
+ * out[i * feature_size * target_frames + m * target_frames + t], zero for
+ * t >= T_i.  target_frames is PreparedChunk::target_frames
+ * (sfe_max_feature_frames(), src/pipeline.rs:160-163).  feature_frames (host,
+ * n entries) receives T_i.  A chunk with T_i > target_frames fails with
+ * SFE_INVALID_ARG ("feature frame count ... exceeded encoder target ...",
+ * src/model.rs:259-264).  Asynchronous on `stream`. */
+int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
+                              int32_t target_frames, int32_t out_dtype, void* out, int64_t* feature_frames,
+                              void* stream);
+
 /* Streaming long-form extraction from HOST memory.  The recording is
  * copied host->device in windows of at most window_samples samples,
  * double-buffered on two streams: the copy of window w+1 overlaps the

@@ -18,7 +18,8 @@ SFE_F32, SFE_BF16 = 0, 1
 EXPORTS = (
     "sfe_config_default", "sfe_overlap_config_default", "sfe_num_frames", "sfe_max_feature_frames",
     "sfe_plan_fast", "sfe_build_tables", "sfe_last_error", "sfe_create", "sfe_destroy", "sfe_extract",
-    "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_streamed",
+    "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_padded",
+    "sfe_extract_chunks_streamed",
     "sfe_set_timing", "sfe_get_timing",
 )
 
@@ -78,6 +79,7 @@ def lib() -> ctypes.CDLL:
         "sfe_prepare_chunk": (ctypes.c_int, [vp, fp, i64, fp, i64, i64p]),
         "sfe_extract_batch": (ctypes.c_int, [vp, vp, i64p, i32, i32, vp, i64p, vp]),
         "sfe_extract_chunks": (ctypes.c_int, [vp, vp, i64, P(SfeChunk), i32, i32, vp, i64p, vp]),
+        "sfe_extract_chunks_padded": (ctypes.c_int, [vp, vp, i64, P(SfeChunk), i32, i32, i32, vp, i64p, vp]),
         "sfe_extract_chunks_streamed": (ctypes.c_int, [vp, fp, i64, P(SfeChunk), i32, i32, vp, i64p, i64]),
         "sfe_set_timing": (ctypes.c_int, [vp, i32]),
         "sfe_get_timing": (ctypes.c_int, [vp, P(ctypes.c_double), P(ctypes.c_double), P(i32)]),

@@ -158,6 +158,7 @@ int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vect
     it.start = starts[i];
     it.len = lens[i];
     it.out_off = (int64_t)sfe::kMel * fo;
+    it.dst_off = it.out_off;
     it.T = (int32_t)T;
     it.tile_off = (int32_t)tiles;
     fo += T;
@@ -198,7 +199,7 @@ hipEvent_t sync_event(sfe_ctx* ctx, size_t i) {
 // log-mel and join the aux stream back into `stream` at the end.  With
 // timing on, every kernel is bracketed by events (read by sfe_get_timing).
 int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Item* d_items, int n, float* raw,
-                void* out, int32_t out_dtype, hipStream_t stream) {
+                void* out, int32_t out_dtype, int pad_to, hipStream_t stream) {
   if (n <= 0) return SFE_OK;
   const int u0 = items[0].tile_off;
   const int u1 = items[n - 1].tile_off + (int)sfe::tiles_for(items[n - 1].T);
@@ -242,7 +243,7 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Ite
       SFE_HIP(hipStreamWaitEvent(ns, done, 0));
     }
     if (e[2]) SFE_HIP(hipEventRecord(e[2], ns));
-    SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, out, bf16, nb > 1, ns));
+    SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, pad_to, out, bf16, nb > 1, ns));
     if (e[3]) SFE_HIP(hipEventRecord(e[3], ns));
     first = last;
   }
@@ -258,7 +259,7 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Ite
 // Uploads items through the pinned staging buffer on `stream`, then runs
 // the log-mel and normalisation kernels.
 int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items, int64_t total_tiles,
-              int64_t total_frames, int32_t out_dtype, void* out, hipStream_t stream) {
+              int64_t total_frames, int32_t out_dtype, void* out, hipStream_t stream, int pad_to = 0) {
   const size_t mbytes = items.size() * sizeof(Item);
   SFE_HIP(ctx->h_meta.reserve(mbytes));
   SFE_HIP(ctx->meta.reserve(mbytes));
@@ -270,7 +271,7 @@ int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items
   SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
   (void)total_tiles;
-  return launch_pair(ctx, samples, items.data(), d_items, (int)items.size(), raw, out, out_dtype, stream);
+  return launch_pair(ctx, samples, items.data(), d_items, (int)items.size(), raw, out, out_dtype, pad_to, stream);
 }
 
 int check_ctx(sfe_ctx* ctx) {
@@ -503,6 +504,39 @@ int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const 
   return run_items(ctx, recording, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
 }
 
+int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
+                              int32_t target_frames, int32_t out_dtype, void* out, int64_t* feature_frames,
+                              void* stream) {
+  if (n <= 0 || !tasks || !recording || !out || !feature_frames || target_frames <= 0)
+    return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+  int rc = check_dtype(out_dtype);
+  if (rc) return rc;
+  std::vector<int64_t> starts(n), lens(n), fo(n + 1);
+  for (int32_t i = 0; i < n; ++i) {
+    const sfe_chunk& t = tasks[i];
+    if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+      return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+    starts[i] = t.audio_start;
+    lens[i] = t.audio_end - t.audio_start;
+  }
+  if ((rc = check_ctx(ctx))) return rc;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  std::vector<Item> items;
+  int64_t tiles = 0;
+  if ((rc = build_items(starts.data(), lens.data(), n, &items, fo.data(), &tiles))) return rc;
+  for (int32_t i = 0; i < n; ++i) {
+    // EncoderInputBuffer::copy_from_features rejects more frames than the
+    // encoder input holds (src/model.rs:259-264)
+    if (items[i].T > target_frames)
+      return fail(SFE_INVALID_ARG, "feature frame count " + std::to_string(items[i].T) + " exceeded encoder target " +
+                                       std::to_string(target_frames));
+    items[i].dst_off = (int64_t)i * sfe::kMel * target_frames;
+    feature_frames[i] = items[i].T;
+  }
+  return run_items(ctx, recording, items, tiles, fo[n], out_dtype, out, static_cast<hipStream_t>(stream),
+                   target_frames);
+}
+
 int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, const sfe_chunk* tasks, int32_t n,
                                 int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples) {
   if (n <= 0 || !tasks || !host || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
@@ -584,7 +618,7 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
     SFE_HIP(hipEventRecord(ctx->ev_copied[b], sx));
     SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[b], 0));
     rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), items.data() + g.first, d_items + g.first, g.count,
-                     raw, out, out_dtype, sc);
+                     raw, out, out_dtype, 0, sc);
     if (rc) return rc;
     SFE_HIP(hipEventRecord(ctx->ev_done[b], sc));
     used[b] = true;

@@ -37,12 +37,14 @@ static_assert(wave_steps(0) <= kMaxSteps && wave_steps(1) <= kMaxSteps && wave_s
               "schedule exceeds the per-wave step budget");
 
 // One featurized item: a clip or a long-form chunk task.  samples[start,
-// start+len) is featurized into out[out_off + m*T + t] (raw log-mel in
+// start+len) is featurized into out[dst_off + m*S + t] (S = T, or the
+// padded row length of the encoder-input layout; raw log-mel in
 // scratch at raw[out_off + t*128 + m], as log2; times ln 2 is the log-mel).
 struct Item {
   int64_t start;
   int64_t len;
-  int64_t out_off;   // element offset = feature_size * frame_offset
+  int64_t out_off;   // raw (scratch) element offset = feature_size * frame_offset
+  int64_t dst_off;   // output element offset: out_off when packed, i * feature_size * pad_to when padded
   int32_t T;         // len / hop + 1
   int32_t tile_off;  // first 16-frame unit of this item, relative to the launch
 };
@@ -79,8 +81,9 @@ constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: o
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
 // frame count (sizes the kernel's register budget).  lean selects the
-// low-footprint variant that co-runs with the log-mel kernel.
-hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, void* out, bool out_bf16,
-                       bool lean, hipStream_t stream);
+// low-footprint variant that co-runs with the log-mel kernel.  pad_to > 0:
+// rows of pad_to frames, zero past T (the encoder input layout).
+hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, int pad_to, void* out,
+                       bool out_bf16, bool lean, hipStream_t stream);
 
 }  // namespace sfe

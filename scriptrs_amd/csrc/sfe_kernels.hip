@@ -664,12 +664,12 @@ __device__ __forceinline__ void put1(uint16_t* o, float y) { *o = f32_to_bf16(y)
 // Store phase of one chunk: its frames are in tb[F][kTStride]
 // (feature-major); wave v writes rows R v .. R v + R - 1 (R = F / W).
 template <int W, int F, typename O>
-__device__ __forceinline__ void store_chunk(const float* tb, const float* st, int t0, int T, int lane, int w,
+__device__ __forceinline__ void store_chunk(const float* tb, const float* st, int t0, int T, int rs, int lane, int w,
                                             O* __restrict__ ob) {
   using S = NormShape<W, F>;
   const int r = S::kRowsPerWave * w + lane / S::kLanesPerRow;
   const float mean = st[3 * r], sd = st[3 * r + 1], rc = st[3 * r + 2];
-  O* orow = ob + (size_t)r * T;
+  O* orow = ob + (size_t)r * rs;
 #pragma unroll
   for (int s = 0; s < S::kChunk / S::kSpan; ++s) {
     const int k = 4 * (lane % S::kLanesPerRow) + S::kSpan * s;
@@ -687,6 +687,14 @@ __device__ __forceinline__ void store_chunk(const float* tb, const float* st, in
   }
 }
 
+// Zeroes frames [T, rs) of the slab's F rows (the encoder-input padding,
+// src/model.rs:266-271).
+template <int W, int F, typename O>
+__device__ __forceinline__ void zero_tail(O* __restrict__ ob, int T, int rs, int lane, int w) {
+  const int tail = rs - T;
+  for (int e = w * 64 + lane; e < F * tail; e += W * 64) put1(ob + (size_t)(e / tail) * rs + T + e % tail, 0.0f);
+}
+
 // Stage one round's float4 (4 features of one frame) of the lane into the
 // transpose buffer at column col.
 template <int W, int F>
@@ -702,7 +710,7 @@ __device__ __forceinline__ void stage(float* tb, int q, int col, const float4& v
 // stream, the lean variant).  `work` is the (item, slab) index.
 template <int W, int F, int N, typename O>
 __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const Item* __restrict__ items,
-                                          int n_items, int work, O* __restrict__ out) {
+                                          int n_items, int work, int pad_to, O* __restrict__ out) {
   static_assert(N % 4 == 0, "whole chunks");
   using S = NormShape<W, F>;
   constexpr int kSpan = S::kSpan;
@@ -722,7 +730,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   const int T = it.T;
   // Uniform bases with 32-bit lane offsets.
   const float* xb = raw + it.out_off + slab;
-  O* ob = out + it.out_off + (size_t)slab * T;
+  const int rs = pad_to > 0 ? pad_to : T;  // output row length
+  O* ob = out + it.dst_off + (size_t)slab * rs;
+  if (pad_to > 0) zero_tail<W, F>(ob, T, rs, lane, w);
   const uint32_t lo = (uint32_t)(fr * kMel + 4 * q);
   const int nr = fr < T ? (T - 1 - fr) / kSpan + 1 : 0;  // rounds holding a frame of this lane
   const float4 x0 = ln2_scale(*reinterpret_cast<const float4*>(xb + 4 * q));
@@ -775,7 +785,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
           for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, v[4 * ch + jr]);
           __syncthreads();
-          store_chunk<W, F>(tb, st, kChunk * ch, T, lane, w, ob);
+          store_chunk<W, F>(tb, st, kChunk * ch, T, rs, lane, w, ob);
           __syncthreads();
         }
       }
@@ -839,7 +849,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     for (int jr = 0; jr < 4; ++jr)
       if (4 * ch + jr < nr) stage<W, F>(tb, q, kSpan * jr + fr, e[jr]);
     __syncthreads();
-    store_chunk<W, F>(tb, st, kChunk * ch, T, lane, w, ob);
+    store_chunk<W, F>(tb, st, kChunk * ch, T, rs, lane, w, ob);
     __syncthreads();
   }
 }
@@ -859,8 +869,8 @@ __device__ __forceinline__ int xcd_pair_work(int b) {
 template <int N, typename O>
 __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const float* __restrict__ raw,
                                                                        const Item* __restrict__ items, int n_items,
-                                                                       O* __restrict__ out) {
-  norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, xcd_pair_work(blockIdx.x), out);
+                                                                       int pad_to, O* __restrict__ out) {
+  norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, xcd_pair_work(blockIdx.x), pad_to, out);
 }
 
 // Lean variant: 4 waves over 32-feature slabs, no register holding (three
@@ -869,8 +879,8 @@ __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const flo
 template <typename O>
 __global__ __launch_bounds__(64 * 4, 5) void sfe_norm_stream_kernel(const float* __restrict__ raw,
                                                                     const Item* __restrict__ items, int n_items,
-                                                                    O* __restrict__ out) {
-  norm_body<4, 32, 0>(raw, items, n_items, blockIdx.x, out);
+                                                                    int pad_to, O* __restrict__ out) {
+  norm_body<4, 32, 0>(raw, items, n_items, blockIdx.x, pad_to, out);
 }
 
 }  // namespace
@@ -887,11 +897,11 @@ hipError_t launch_logmel(const float* samples, const Item* items, int n_items, i
 }
 
 template <typename O>
-hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, O* out, bool lean,
+hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, int pad_to, O* out, bool lean,
                          hipStream_t stream) {
   if (lean) {
     const unsigned blocks = (unsigned)((int64_t)n_items * NormShape<4, 32>::kSlabs);
-    sfe_norm_stream_kernel<O><<<dim3(blocks), dim3(64 * 4), 0, stream>>>(raw, items, n_items, out);
+    sfe_norm_stream_kernel<O><<<dim3(blocks), dim3(64 * 4), 0, stream>>>(raw, items, n_items, pad_to, out);
     return hipGetLastError();
   }
   using S = NormShape<kNormMainWaves, kNormMainSlab>;
@@ -900,18 +910,18 @@ hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int m
   const dim3 grid(blocks), block(S::kThreads);
   // Registers per lane sized to the longest item (N float4s hold kSpan N
   // frames); longer items take the streaming path.
-  if (max_T <= S::kSpan * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else if (max_T <= S::kSpan * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else if (max_T <= S::kSpan * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
-  else sfe_norm_kernel<32, O><<<grid, block, 0, stream>>>(raw, items, n_items, out);
+  if (max_T <= S::kSpan * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  else if (max_T <= S::kSpan * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  else if (max_T <= S::kSpan * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  else sfe_norm_kernel<32, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
   return hipGetLastError();
 }
 
-hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, void* out, bool out_bf16,
-                       bool lean, hipStream_t stream) {
+hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, int pad_to, void* out,
+                       bool out_bf16, bool lean, hipStream_t stream) {
   if (n_items <= 0) return hipSuccess;
-  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, static_cast<uint16_t*>(out), lean, stream);
-  return launch_norm_t(raw, items, n_items, max_T, static_cast<float*>(out), lean, stream);
+  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, pad_to, static_cast<uint16_t*>(out), lean, stream);
+  return launch_norm_t(raw, items, n_items, max_T, pad_to, static_cast<float*>(out), lean, stream);
 }
 
 }  // namespace sfe

@@ -206,6 +206,26 @@ class ParakeetFeatureExtractor:
         _check(rc)
         return out, fo
 
+    def extract_chunks_encoder_input(self, recording, tasks, target_frames: int | None = None, dtype: str = "f32",
+                                     stream=None, out=None):
+        """Featurize chunk tasks straight into the encoder input layout: a
+        device tensor [n, 128, target_frames], feature-major, zero past each
+        chunk's frame count -- what ``EncoderInputBuffer::copy_from_features``
+        builds on the host (src/model.rs:241-278).  ``target_frames`` defaults
+        to ``max_feature_frames()`` (``PreparedChunk::target_frames``,
+        src/pipeline.rs:160-163).  Returns ``(out, feature_frames)``."""
+        import torch
+        arr, n = _tasks_array(tasks)
+        tf = int(target_frames or self.config.max_feature_frames())
+        ff = np.zeros(n, np.int64)
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        if out is None:
+            out = torch.empty((n, self.config.feature_size, tf), dtype=tdt, device=recording.device)
+        rc = _lib.lib().sfe_extract_chunks_padded(self._handle(), _dev_ptr(recording), recording.numel(), arr, n, tf,
+                                                  _dtype_code(dtype), _dev_ptr(out), _ip(ff), _stream_handle(stream))
+        _check(rc)
+        return out, ff
+
     def extract_chunks_streamed(self, host_recording: np.ndarray, tasks, window_samples: int = 960_000,
                                 dtype: str = "f32", out=None):
         """Streamed long-form extraction: the recording stays in host memory and

@@ -146,3 +146,39 @@ def test_long_form_batched_pipeline(extractor):
         a = rec[starts[i]:starts[i] + lens[i]]
         got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
         assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
+
+
+def test_encoder_input_layout(extractor):
+    """sfe_extract_chunks_padded writes what EncoderInputBuffer::copy_from_features
+    builds (src/model.rs:241-278): per chunk [128, target_frames], the packed
+    features in the first T columns, zeros after; bit-identical to the packed
+    output of sfe_extract_chunks."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: encoder input layout")
+    rec = synth.speech_like(1_300_000, 17)
+    tasks = build_fast_execution_plan(rec.size)
+    dev = torch.from_numpy(rec).cuda()
+    packed, fo = extractor.extract_chunks(dev, tasks)
+    enc, ff = extractor.extract_chunks_encoder_input(dev, tasks)
+    torch.cuda.synchronize()
+    packed = packed.cpu().numpy()
+    enc = enc.cpu().numpy()
+    assert enc.shape == (len(tasks), 128, 1501)
+    assert np.array_equal(ff, np.diff(fo))
+    for i in range(len(tasks)):
+        T = int(ff[i])
+        want = packed[128 * fo[i]:128 * fo[i + 1]].reshape(128, T)
+        assert np.array_equal(enc[i, :, :T], want), i
+        assert not enc[i, :, T:].any(), i
+
+
+def test_encoder_input_rejects_overlong_chunk(extractor):
+    import torch
+    from scriptrs_amd import ChunkTask
+    from scriptrs_amd.frontend import InvalidModelOutput
+    _flush("case: encoder input overlong chunk")
+    rec = synth.sinusoids(400_000, 3)
+    dev = torch.from_numpy(rec).cuda()
+    with pytest.raises(InvalidModelOutput, match="exceeded encoder target"):
+        extractor.extract_chunks_encoder_input(dev, [ChunkTask(0, 300_000, 0, 0)])
