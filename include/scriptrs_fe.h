@@ -47,6 +47,13 @@ typedef enum sfe_status {
 
 typedef enum sfe_dtype { SFE_F32 = 0, SFE_BF16 = 1 } sfe_dtype;
 
+/* Input sample formats.  Integer PCM is decoded in the kernel exactly as the
+ * reference's WAV reader does (examples/transcribe_wav.rs:342-348,
+ * dev-tools/src/bin/compare_parakeet_rs.rs:540-546): value as f32 divided by
+ * ((1 << (bits_per_sample - 1)) - 1) as f32, correctly rounded.  SFE_PCM_I16
+ * holds samples of 2..16 bits in int16, SFE_PCM_I32 2..32 bits in int32. */
+typedef enum sfe_pcm { SFE_PCM_F32 = 0, SFE_PCM_I16 = 1, SFE_PCM_I32 = 2 } sfe_pcm;
+
 /* Mirrors TranscriptionConfig (src/config.rs:11-28, defaults :30-44). */
 typedef struct sfe_config {
   int32_t sample_rate;               /* 16000 */
@@ -156,6 +163,16 @@ int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets
 int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
                        int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream);
 
+/* sfe_extract_chunks over a device recording in PCM format `pcm_format`
+ * (sfe_pcm; bits_per_sample is ignored for SFE_PCM_F32).  The decode to f32
+ * (the WAV reader's int -> f32 scaling, examples/transcribe_wav.rs:342-348)
+ * is fused into the log-mel kernel's sample loads, so 16-bit input moves half
+ * the bytes of f32.  Results equal sfe_extract_chunks on the decoded
+ * samples. */
+int sfe_extract_chunks_pcm(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample,
+                           int64_t len, const sfe_chunk* tasks, int32_t n, int32_t out_dtype, void* out,
+                           int64_t* frame_offsets, void* stream);
+
 /* Encoder-ready long-form extraction: as sfe_extract_chunks, but chunk i is
  * written in the encoder input layout that EncoderInputBuffer::
  * copy_from_features builds on the host (src/model.rs:241-278):
@@ -180,6 +197,14 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
 int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host_recording, int64_t len, const sfe_chunk* tasks,
                                 int32_t n, int32_t out_dtype, void* out, int64_t* frame_offsets,
                                 int64_t window_samples);
+
+/* sfe_extract_chunks_streamed over a host recording in PCM format
+ * `pcm_format` (see sfe_extract_chunks_pcm): integer PCM crosses PCIe at its
+ * own width (2 bytes per sample for 16-bit audio) and is decoded on the
+ * GPU. */
+int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, int32_t pcm_format,
+                                    int32_t bits_per_sample, int64_t len, const sfe_chunk* tasks, int32_t n,
+                                    int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples);
 
 /* ---- instrumentation (no reference counterpart) ----------------------- */
 

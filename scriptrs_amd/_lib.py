@@ -13,13 +13,14 @@ LIB_PATH = os.path.join(_HERE, "libscriptrs_fe.so")
 
 SFE_OK, SFE_EMPTY_AUDIO, SFE_INVALID_ARG, SFE_HIP_ERROR, SFE_AUDIO_TOO_LONG = 0, 1, 2, 3, 4
 SFE_F32, SFE_BF16 = 0, 1
+SFE_PCM_F32, SFE_PCM_I16, SFE_PCM_I32 = 0, 1, 2
 
 # Every symbol include/scriptrs_fe.h declares.
 EXPORTS = (
     "sfe_config_default", "sfe_overlap_config_default", "sfe_num_frames", "sfe_max_feature_frames",
     "sfe_plan_fast", "sfe_build_tables", "sfe_last_error", "sfe_create", "sfe_destroy", "sfe_extract",
-    "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_padded",
-    "sfe_extract_chunks_streamed",
+    "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_pcm",
+    "sfe_extract_chunks_padded", "sfe_extract_chunks_streamed", "sfe_extract_chunks_streamed_pcm",
     "sfe_set_timing", "sfe_get_timing",
 )
 
@@ -79,6 +80,9 @@ def lib() -> ctypes.CDLL:
         "sfe_prepare_chunk": (ctypes.c_int, [vp, fp, i64, fp, i64, i64p]),
         "sfe_extract_batch": (ctypes.c_int, [vp, vp, i64p, i32, i32, vp, i64p, vp]),
         "sfe_extract_chunks": (ctypes.c_int, [vp, vp, i64, P(SfeChunk), i32, i32, vp, i64p, vp]),
+        "sfe_extract_chunks_pcm": (ctypes.c_int, [vp, vp, i32, i32, i64, P(SfeChunk), i32, i32, vp, i64p, vp]),
+        "sfe_extract_chunks_streamed_pcm": (ctypes.c_int, [vp, vp, i32, i32, i64, P(SfeChunk), i32, i32, vp, i64p,
+                                                           i64]),
         "sfe_extract_chunks_padded": (ctypes.c_int, [vp, vp, i64, P(SfeChunk), i32, i32, i32, vp, i64p, vp]),
         "sfe_extract_chunks_streamed": (ctypes.c_int, [vp, fp, i64, P(SfeChunk), i32, i32, vp, i64p, i64]),
         "sfe_set_timing": (ctypes.c_int, [vp, i32]),

@@ -20,6 +20,14 @@ using sfe::Item;
 
 namespace {
 
+// Where the samples come from: f32, or integer PCM decoded in the kernel.
+struct Source {
+  const void* ptr;
+  int pcm;      // sfe::kPcm*
+  float scale;  // PCM decode divisor
+  size_t esize;
+};
+
 // Batching of one launch (see launch_pair).
 constexpr int kMaxBatches = 1;  // batching measured slower (see launch_pair); kept off
 constexpr int kMinUnitsPerBatch = 4096;  // 16-frame units; smaller calls run unbatched
@@ -198,7 +206,7 @@ hipEvent_t sync_event(sfe_ctx* ctx, size_t i) {
 // fit on a CU together.  Events order each normalisation after its batch's
 // log-mel and join the aux stream back into `stream` at the end.  With
 // timing on, every kernel is bracketed by events (read by sfe_get_timing).
-int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Item* d_items, int n, float* raw,
+int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d_items, int n, float* raw,
                 void* out, int32_t out_dtype, int pad_to, hipStream_t stream) {
   if (n <= 0) return SFE_OK;
   const int u0 = items[0].tile_off;
@@ -233,7 +241,8 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Ite
       for (int i = 0; i < 4; ++i)
         if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
     if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
-    SFE_HIP(sfe::launch_logmel(samples, d_items + first, cnt, bu0, bu1 - bu0, ctx->d_tables, ctx->cfg.preemphasis, raw,
+    SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_items + first, cnt, bu0, bu1 - bu0, ctx->d_tables,
+                               ctx->cfg.preemphasis, raw,
                                ctx->grid_cap, stream));
     if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
     if (nb > 1) {
@@ -258,7 +267,7 @@ int launch_pair(sfe_ctx* ctx, const float* samples, const Item* items, const Ite
 
 // Uploads items through the pinned staging buffer on `stream`, then runs
 // the log-mel and normalisation kernels.
-int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items, int64_t total_tiles,
+int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, int64_t total_tiles,
               int64_t total_frames, int32_t out_dtype, void* out, hipStream_t stream, int pad_to = 0) {
   const size_t mbytes = items.size() * sizeof(Item);
   SFE_HIP(ctx->h_meta.reserve(mbytes));
@@ -271,7 +280,26 @@ int run_items(sfe_ctx* ctx, const float* samples, const std::vector<Item>& items
   SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
   (void)total_tiles;
-  return launch_pair(ctx, samples, items.data(), d_items, (int)items.size(), raw, out, out_dtype, pad_to, stream);
+  return launch_pair(ctx, src, items.data(), d_items, (int)items.size(), raw, out, out_dtype, pad_to, stream);
+}
+
+Source f32_source(const float* p) { return Source{p, sfe::kPcmF32, 1.0f, sizeof(float)}; }
+
+// The reference's WAV decode divisor: ((1 << (bits - 1)) - 1) as f32
+// (examples/transcribe_wav.rs:342-343).  Widths below 2 bits (a zero
+// divisor) are rejected.
+int pcm_source(const void* p, int32_t pcm, int32_t bits, Source* out) {
+  if (pcm == SFE_PCM_F32) {
+    *out = f32_source(static_cast<const float*>(p));
+    return SFE_OK;
+  }
+  const int maxbits = pcm == SFE_PCM_I16 ? 16 : (pcm == SFE_PCM_I32 ? 32 : 0);
+  if (!maxbits) return fail(SFE_INVALID_ARG, "pcm_format must be SFE_PCM_F32, SFE_PCM_I16 or SFE_PCM_I32");
+  if (bits < 2 || bits > maxbits)
+    return fail(SFE_INVALID_ARG, "bits_per_sample must be in [2, " + std::to_string(maxbits) + "] for this pcm_format");
+  const float scale = (float)((((int64_t)1) << (bits - 1)) - 1);
+  *out = Source{p, pcm == SFE_PCM_I16 ? sfe::kPcmI16 : sfe::kPcmI32, scale, pcm == SFE_PCM_I16 ? 2u : 4u};
+  return SFE_OK;
 }
 
 int check_ctx(sfe_ctx* ctx) {
@@ -441,7 +469,7 @@ int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64
   std::vector<Item> items;
   int64_t start = 0, tiles = 0, fo[2];
   if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
-  if ((rc = run_items(ctx, static_cast<float*>(ctx->io_in.ptr), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
+  if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
     return rc;
   SFE_HIP(hipMemcpyAsync(out, ctx->io_out.ptr, (size_t)nout * sizeof(float), hipMemcpyDeviceToHost, s));
   SFE_HIP(hipStreamSynchronize(s));
@@ -480,14 +508,23 @@ int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets
   std::vector<Item> items;
   int64_t tiles = 0;
   if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-  return run_items(ctx, samples, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+  return run_items(ctx, f32_source(samples), items, tiles, frame_offsets[n], out_dtype, out,
+                   static_cast<hipStream_t>(stream));
 }
 
 int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
                        int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream) {
+  return sfe_extract_chunks_pcm(ctx, recording, SFE_PCM_F32, 32, len, tasks, n, out_dtype, out, frame_offsets, stream);
+}
+
+int sfe_extract_chunks_pcm(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample,
+                           int64_t len, const sfe_chunk* tasks, int32_t n, int32_t out_dtype, void* out,
+                           int64_t* frame_offsets, void* stream) {
   if (n <= 0 || !tasks || !recording || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
   int rc = check_dtype(out_dtype);
   if (rc) return rc;
+  Source src;
+  if ((rc = pcm_source(recording, pcm_format, bits_per_sample, &src))) return rc;
   std::vector<int64_t> starts(n), lens(n);
   for (int32_t i = 0; i < n; ++i) {
     const sfe_chunk& t = tasks[i];
@@ -501,7 +538,7 @@ int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const 
   std::vector<Item> items;
   int64_t tiles = 0;
   if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-  return run_items(ctx, recording, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+  return run_items(ctx, src, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
 }
 
 int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
@@ -533,15 +570,26 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
     items[i].dst_off = (int64_t)i * sfe::kMel * target_frames;
     feature_frames[i] = items[i].T;
   }
-  return run_items(ctx, recording, items, tiles, fo[n], out_dtype, out, static_cast<hipStream_t>(stream),
+  return run_items(ctx, f32_source(recording), items, tiles, fo[n], out_dtype, out, static_cast<hipStream_t>(stream),
                    target_frames);
 }
 
 int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, const sfe_chunk* tasks, int32_t n,
                                 int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples) {
+  return sfe_extract_chunks_streamed_pcm(ctx, host, SFE_PCM_F32, 32, len, tasks, n, out_dtype, out, frame_offsets,
+                                         window_samples);
+}
+
+int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, int32_t pcm_format,
+                                    int32_t bits_per_sample, int64_t len, const sfe_chunk* tasks, int32_t n,
+                                    int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples) {
+  const char* host = static_cast<const char*>(host_recording);
   if (n <= 0 || !tasks || !host || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
   int rc = check_dtype(out_dtype);
   if (rc) return rc;
+  Source src;
+  if ((rc = pcm_source(host_recording, pcm_format, bits_per_sample, &src))) return rc;
+  const size_t es = src.esize;
   std::vector<int64_t> starts(n), lens(n);
   for (int32_t i = 0; i < n; ++i) {
     const sfe_chunk& t = tasks[i];
@@ -593,8 +641,8 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
   SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
   for (int b = 0; b < 2; ++b) {
-    SFE_HIP(ctx->win[b].reserve((size_t)window_samples * sizeof(float)));
-    SFE_HIP(ctx->h_win[b].reserve((size_t)window_samples * sizeof(float)));
+    SFE_HIP(ctx->win[b].reserve((size_t)window_samples * es));
+    SFE_HIP(ctx->h_win[b].reserve((size_t)window_samples * es));
   }
   hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
   memcpy(ctx->h_meta.ptr, items.data(), mbytes);
@@ -606,10 +654,10 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
   for (size_t gi = 0; gi < groups.size(); ++gi) {
     const Group& g = groups[gi];
     const int b = (int)(gi & 1);
-    const size_t bytes = (size_t)(g.wend - g.wstart) * sizeof(float);
+    const size_t bytes = (size_t)(g.wend - g.wstart) * es;
     // the pinned buffer is free once its previous H2D copy has finished
     SFE_HIP(ctx->h_win[b].wait());
-    memcpy(ctx->h_win[b].ptr, host + g.wstart, bytes);
+    memcpy(ctx->h_win[b].ptr, host + (size_t)g.wstart * es, bytes);
     // the device window is free once the kernels that read it have finished
     if (used[b]) SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_done[b], 0));
     SFE_HIP(hipMemcpyAsync(ctx->win[b].ptr, ctx->h_win[b].ptr, bytes, hipMemcpyHostToDevice, sx));
@@ -617,7 +665,9 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
     ctx->h_win[b].pending = true;
     SFE_HIP(hipEventRecord(ctx->ev_copied[b], sx));
     SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[b], 0));
-    rc = launch_pair(ctx, static_cast<const float*>(ctx->win[b].ptr), items.data() + g.first, d_items + g.first, g.count,
+    Source wsrc = src;
+    wsrc.ptr = ctx->win[b].ptr;
+    rc = launch_pair(ctx, wsrc, items.data() + g.first, d_items + g.first, g.count,
                      raw, out, out_dtype, 0, sc);
     if (rc) return rc;
     SFE_HIP(hipEventRecord(ctx->ev_done[b], sc));

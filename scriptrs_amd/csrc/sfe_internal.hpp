@@ -72,9 +72,15 @@ constexpr int kTile = 16;  // frames per unit of work (one pass) of the log-mel 
 int64_t tiles_for(int64_t T);
 // grid_cap: workgroups resident on the device at once (the kernel loops
 // over tiles, so launching more than that only adds scheduling overhead).
+// Input sample formats: f32, or integer PCM (16-bit or 32-bit containers)
+// decoded as value / pcm_scale in the kernel.
+constexpr int kPcmF32 = 0;
+constexpr int kPcmI16 = 1;
+constexpr int kPcmI32 = 2;
 // Units [unit0, unit0 + n_units) in the numbering of items[].tile_off.
-hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int unit0, int n_units,
-                         const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream);
+hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
+                         int n_units, const DevTables* tables, float preemph, float* raw_out, int grid_cap,
+                         hipStream_t stream);
 constexpr int kLogmelWavesPerSimd = 2;
 constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
 // Normalises raw (f32 log2 values, frame-major [T][128] per item) per (item, feature)

@@ -133,18 +133,64 @@ static_assert(kSpan <= kWaveBuf, "span must fit the wave buffer");
 constexpr int kSpanVec = (kSpan + 255) / 256;  // 16-byte loads per lane (4)
 static_assert(kSpan % 4 == 0, "span is whole float4s");
 
+// Input samples: f32, or integer PCM decoded as the reference's WAV reader
+// does (examples/transcribe_wav.rs:342-348): value as f32 / scale with
+// scale = ((1 << (bits - 1)) - 1) as f32.  The division is correctly rounded
+// by one residual step from r = RN(1 / scale): q = RN(v r) is within an ulp
+// of v / scale, and q + r fma(-scale, q, v) rounds to RN(v / scale)
+// (Markstein; checked exhaustively for 16-bit PCM by the tests).
+struct Decode {
+  float scale, recip;
+};
+
+__device__ __forceinline__ float pcm_div(float v, const Decode& d) {
+#pragma clang fp contract(off)  // q is the rounded product
+  const float q = v * d.recip;
+  return __fmaf_rn(__fmaf_rn(-d.scale, q, v), d.recip, q);
+}
+
+template <typename S>
+struct Pcm;
+template <>
+struct Pcm<float> {
+  using V4 = float4;  // 4 raw samples
+  static __device__ __forceinline__ V4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  static __device__ __forceinline__ float dec(float v, const Decode&) { return v; }
+  static __device__ __forceinline__ float4 dec4(const V4& v, const Decode&) { return v; }
+};
+template <>
+struct Pcm<int16_t> {
+  typedef short V4 __attribute__((ext_vector_type(4), aligned(2)));
+  static __device__ __forceinline__ V4 load4(const int16_t* p) { return *reinterpret_cast<const V4*>(p); }
+  static __device__ __forceinline__ float dec(int16_t v, const Decode& d) { return pcm_div((float)v, d); }
+  static __device__ __forceinline__ float4 dec4(const V4& v, const Decode& d) {
+    return make_float4(pcm_div((float)v.x, d), pcm_div((float)v.y, d), pcm_div((float)v.z, d), pcm_div((float)v.w, d));
+  }
+};
+template <>
+struct Pcm<int32_t> {
+  typedef int V4 __attribute__((ext_vector_type(4), aligned(4)));
+  static __device__ __forceinline__ V4 load4(const int32_t* p) { return *reinterpret_cast<const V4*>(p); }
+  static __device__ __forceinline__ float dec(int32_t v, const Decode& d) { return pcm_div((float)v, d); }
+  static __device__ __forceinline__ float4 dec4(const V4& v, const Decode& d) {
+    return make_float4(pcm_div((float)v.x, d), pcm_div((float)v.y, d), pcm_div((float)v.z, d), pcm_div((float)v.w, d));
+  }
+};
+
 // The 880 samples under one wave's 4 frames of a unit: span sample j is
 // item sample s0 + j, valid for j in [jlo, jhi).
+template <typename S>
 struct Span {
-  const float* xb;
+  const S* xb;
   int64_t s0;
   int jlo, jhi;
   bool interior;  // the whole span lies inside the item, after its first sample
 };
 
-__device__ __forceinline__ Span make_span(const Item& it, const float* samples, int u, int w) {
+template <typename S>
+__device__ __forceinline__ Span<S> make_span(const Item& it, const S* samples, int u, int w) {
   const int fw = (u - it.tile_off) * kPassFrames + 4 * w;
-  Span sp;
+  Span<S> sp;
   sp.s0 = (int64_t)fw * kHop - kPad;
   sp.jlo = sp.s0 < 0 ? (int)(-sp.s0) : 0;
   sp.jhi = (int)(it.len - sp.s0 < (int64_t)kSpan ? (it.len - sp.s0 > 0 ? it.len - sp.s0 : 0) : (int64_t)kSpan);
@@ -153,17 +199,19 @@ __device__ __forceinline__ Span make_span(const Item& it, const float* samples, 
   return sp;
 }
 
-// Issues the 16-byte loads of an interior span (lane L: samples 4L + 256 h
-// + 0..3) and, per lane, the sample before its first vector (4L - 1), which
-// is that vector's preemphasis neighbour.  The per-lane address keeps it a
-// vector load: a scalar load would share lgkmcnt with LDS, and every later
-// LDS wait would also wait for it.  Other spans are read when processed.
-__device__ __forceinline__ void prefetch_span(const Span& sp, int lane, float4 (&v)[kSpanVec], float& xm1) {
+// Issues the loads of an interior span (lane L: samples 4L + 256 h + 0..3)
+// and, per lane, the sample before its first vector (4L - 1), which is that
+// vector's preemphasis neighbour.  The per-lane address keeps it a vector
+// load: a scalar load would share lgkmcnt with LDS, and every later LDS wait
+// would also wait for it.  Other spans are read when processed.  Samples
+// stay raw (undecoded) in registers until used.
+template <typename S>
+__device__ __forceinline__ void prefetch_span(const Span<S>& sp, int lane, typename Pcm<S>::V4 (&v)[kSpanVec], S& xm1) {
   if (!sp.interior) return;
 #pragma unroll
   for (int h = 0; h < kSpanVec; ++h) {
     const int j = 4 * lane + 256 * h;
-    v[h] = *reinterpret_cast<const float4*>(sp.xb + (j < kSpan ? j : 0));
+    v[h] = Pcm<S>::load4(sp.xb + (j < kSpan ? j : 0));
   }
   xm1 = sp.xb[4 * lane - 1];
 }
@@ -264,11 +312,12 @@ __device__ __forceinline__ void store_pending(int w, const MelAcc& acc, float* f
   }
 }
 
-__global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kernel(const float* __restrict__ samples,
+template <typename S>
+__global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kernel(const S* __restrict__ samples,
                                                               const Item* __restrict__ items, int n_items,
                                                               int unit0, int n_units,
                                                               const DevTables* __restrict__ tb, float coef,
-                                                              float* __restrict__ out) {
+                                                              Decode dc, float* __restrict__ out) {
   __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
   __shared__ __align__(16) float pbuf[2][kPassFrames][kPStride];
 
@@ -340,9 +389,9 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
   Item it_n = items[li + 1 < n_items ? li + 1 : li];
   // The samples of unit u + 1 are loaded into registers while unit u is
   // transformed, so the global-load latency hides behind the FFT.
-  Span sp_n = make_span(it_c, samples, u_begin, w);
-  float4 nv[kSpanVec];
-  float nxm1 = 0.0f;
+  Span<S> sp_n = make_span(it_c, samples, u_begin, w);
+  typename Pcm<S>::V4 nv[kSpanVec] = {};
+  S nxm1 = 0;
   prefetch_span(sp_n, lane, nv, nxm1);
 
   MelAcc acc;
@@ -351,11 +400,13 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
 
   for (int u = u_begin; u < u_end; ++u) {
     const Item it = it_c;
-    const Span sp = sp_n;
+    const Span<S> sp = sp_n;
+    // (for a span that is not interior nv holds stale values, decoded and
+    // never used)
     float4 cv[kSpanVec];
 #pragma unroll
-    for (int h = 0; h < kSpanVec; ++h) cv[h] = nv[h];
-    const float cxm1 = nxm1;
+    for (int h = 0; h < kSpanVec; ++h) cv[h] = Pcm<S>::dec4(nv[h], dc);
+    const float cxm1 = Pcm<S>::dec(nxm1, dc);
     const int T = it.T;
     const int f0 = (u - it.tile_off) * kPassFrames;
     float* o = out + it.out_off;
@@ -396,9 +447,9 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
             const int je = j + e;
             float v = 0.0f;
             if (je >= sp.jlo && je < sp.jhi) {
-              const float cur = sp.xb[je];
+              const float cur = Pcm<S>::dec(sp.xb[je], dc);
               // item sample 0 (je == jlo with the span starting before the item)
-              v = (je == sp.jlo && sp.s0 <= 0) ? cur : cur - coef * sp.xb[je - 1];
+              v = (je == sp.jlo && sp.s0 <= 0) ? cur : cur - coef * Pcm<S>::dec(sp.xb[je - 1], dc);
             }
             y[e] = v;
           }
@@ -887,12 +938,22 @@ __global__ __launch_bounds__(64 * 4, 5) void sfe_norm_stream_kernel(const float*
 
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
 
-hipError_t launch_logmel(const float* samples, const Item* items, int n_items, int unit0, int n_units,
-                         const DevTables* tables, float preemph, float* raw_out, int grid_cap, hipStream_t stream) {
+hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
+                         int n_units, const DevTables* tables, float preemph, float* raw_out, int grid_cap,
+                         hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
   const int grid = n_units < grid_cap ? n_units : grid_cap;
-  sfe_logmel_kernel<<<dim3(grid), dim3(kThreads), 0, stream>>>(samples, items, n_items, unit0, n_units, tables,
-                                                                preemph, raw_out);
+  Decode dc{pcm_scale, 1.0f / pcm_scale};  // the host's division is correctly rounded
+  const dim3 g(grid), b(kThreads);
+  if (pcm == kPcmI16)
+    sfe_logmel_kernel<int16_t><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items, unit0,
+                                                    n_units, tables, preemph, dc, raw_out);
+  else if (pcm == kPcmI32)
+    sfe_logmel_kernel<int32_t><<<g, b, 0, stream>>>(static_cast<const int32_t*>(samples), items, n_items, unit0,
+                                                    n_units, tables, preemph, dc, raw_out);
+  else
+    sfe_logmel_kernel<float><<<g, b, 0, stream>>>(static_cast<const float*>(samples), items, n_items, unit0, n_units,
+                                                  tables, preemph, dc, raw_out);
   return hipGetLastError();
 }
 

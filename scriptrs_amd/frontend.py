@@ -206,6 +206,26 @@ class ParakeetFeatureExtractor:
         _check(rc)
         return out, fo
 
+    def extract_chunks_pcm(self, recording, tasks, bits_per_sample: int | None = None, dtype: str = "f32",
+                           stream=None, out=None):
+        """``extract_chunks`` over a device recording of integer PCM (torch.int16
+        or torch.int32), decoded in the kernel as the reference's WAV reader
+        does: ``value as f32 / ((1 << (bits - 1)) - 1) as f32``
+        (examples/transcribe_wav.rs:342-348).  ``bits_per_sample`` defaults to
+        the container width."""
+        import torch
+        pcm, bits = _pcm_format(recording.dtype, bits_per_sample)
+        arr, n = _tasks_array(tasks)
+        fo = np.zeros(n + 1, np.int64)
+        fo[1:] = np.cumsum([(t.audio_end - t.audio_start) // self.config.hop_length + 1 for t in arr])
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        if out is None:
+            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=recording.device)
+        rc = _lib.lib().sfe_extract_chunks_pcm(self._handle(), _dev_ptr(recording), pcm, bits, recording.numel(), arr,
+                                               n, _dtype_code(dtype), _dev_ptr(out), _ip(fo), _stream_handle(stream))
+        _check(rc)
+        return out, fo
+
     def extract_chunks_encoder_input(self, recording, tasks, target_frames: int | None = None, dtype: str = "f32",
                                      stream=None, out=None):
         """Featurize chunk tasks straight into the encoder input layout: a
@@ -227,21 +247,39 @@ class ParakeetFeatureExtractor:
         return out, ff
 
     def extract_chunks_streamed(self, host_recording: np.ndarray, tasks, window_samples: int = 960_000,
-                                dtype: str = "f32", out=None):
+                                dtype: str = "f32", out=None, bits_per_sample: int | None = None):
         """Streamed long-form extraction: the recording stays in host memory and
-        is copied in double-buffered windows of ``window_samples`` samples."""
+        is copied in double-buffered windows of ``window_samples`` samples.
+        float32, int16 or int32 PCM; integer PCM crosses PCIe at its own width
+        and is decoded on the GPU (see ``extract_chunks_pcm``)."""
         import torch
-        h = np.ascontiguousarray(host_recording, np.float32)
+        h = np.ascontiguousarray(host_recording)
+        if h.dtype not in (np.float32, np.int16, np.int32):
+            h = h.astype(np.float32)
+        pcm, bits = _pcm_format(h.dtype, bits_per_sample)
         arr, n = _tasks_array(tasks)
         fo = np.zeros(n + 1, np.int64)
         fo[1:] = np.cumsum([(t.audio_end - t.audio_start) // self.config.hop_length + 1 for t in arr])
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
             out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=f"cuda:{self.device}")
-        rc = _lib.lib().sfe_extract_chunks_streamed(self._handle(), _fp(h), h.size, arr, n, _dtype_code(dtype),
-                                                    _dev_ptr(out), _ip(fo), int(window_samples))
+        rc = _lib.lib().sfe_extract_chunks_streamed_pcm(self._handle(), h.ctypes.data_as(ctypes.c_void_p), pcm, bits,
+                                                        h.size, arr, n, _dtype_code(dtype), _dev_ptr(out), _ip(fo),
+                                                        int(window_samples))
         _check(rc)
         return out, fo
+
+
+def _pcm_format(dtype, bits):
+    """(sfe_pcm code, bits_per_sample) for a numpy or torch sample dtype."""
+    name = str(dtype).replace("torch.", "")
+    if name == "float32":
+        return _lib.SFE_PCM_F32, 32
+    if name == "int16":
+        return _lib.SFE_PCM_I16, int(bits or 16)
+    if name == "int32":
+        return _lib.SFE_PCM_I32, int(bits or 32)
+    raise InvalidModelOutput(f"unsupported sample dtype {name}")
 
 
 def _dtype_code(dtype: str) -> int:

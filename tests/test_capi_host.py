@@ -145,3 +145,61 @@ def test_unsupported_dtype_rejected_before_device():
     with pytest.raises(InvalidModelOutput):
         from scriptrs_amd.frontend import _dtype_code
         _dtype_code("f16")
+
+
+def _rn32(x):
+    """Exact rounding of a rational to float32 (nearest, ties to even)."""
+    from fractions import Fraction
+    c = np.float32(float(x))
+    best = None
+    for v in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        key = (abs(Fraction(float(v)) - x), int(np.float32(v).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, np.float32(v))
+    return best[1]
+
+
+def _residual_div(v, scale, recip):
+    """The kernel's PCM decode: q = RN(v r); RN(q + r RN(v - scale q)) with
+    both steps fused multiply-adds (exact products, one rounding each)."""
+    from fractions import Fraction
+    a, s, r = np.float32(v), np.float32(scale), np.float32(recip)
+    q = np.float32(a * r)
+    e = _rn32(Fraction(float(a)) - Fraction(float(s)) * Fraction(float(q)))
+    return _rn32(Fraction(float(q)) + Fraction(float(e)) * Fraction(float(r)))
+
+
+def test_pcm_decode_is_correctly_rounded_for_every_int16():
+    """The in-kernel decode of 16-bit PCM equals the reference's f32 division
+    value as f32 / 32767.0 (examples/transcribe_wav.rs:342-348) for all
+    65536 inputs: the residual step reproduces IEEE division exactly."""
+    scale = np.float32(32767.0)
+    recip = np.float32(1.0) / scale
+    v = np.arange(-32768, 32768, dtype=np.float32)
+    want = v / scale  # numpy's f32 division is correctly rounded
+    q = v * recip
+    # fast exact screen: where q already equals the quotient nothing can go wrong
+    todo = np.nonzero(q != want)[0]
+    for i in todo:
+        assert _residual_div(v[i], scale, recip) == want[i], int(v[i])
+
+
+def test_pcm_decode_24_bit_sample():
+    rng = np.random.default_rng(5)
+    scale = np.float32(float((1 << 23) - 1))
+    recip = np.float32(1.0) / scale
+    vals = rng.integers(-(1 << 23), 1 << 23, 4000).astype(np.float32)
+    for v in vals:
+        assert _residual_div(v, scale, recip) == np.float32(v) / scale, v
+
+
+def test_pcm_argument_errors_before_device():
+    from scriptrs_amd._lib import SfeChunk
+    L = _lib.lib()
+    t = (SfeChunk * 1)(SfeChunk(0, 1000, 0, 0))
+    fo = (ctypes.c_int64 * 2)()
+    buf = (ctypes.c_int16 * 1000)()
+    for fmt, bits in ((1, 1), (1, 17), (2, 33), (7, 16)):
+        rc = L.sfe_extract_chunks_pcm(None, ctypes.cast(buf, ctypes.c_void_p), fmt, bits, 1000, t, 1, 0,
+                                      ctypes.cast(buf, ctypes.c_void_p), fo, None)
+        assert rc == _lib.SFE_INVALID_ARG, (fmt, bits)

@@ -182,3 +182,50 @@ def test_encoder_input_rejects_overlong_chunk(extractor):
     dev = torch.from_numpy(rec).cuda()
     with pytest.raises(InvalidModelOutput, match="exceeded encoder target"):
         extractor.extract_chunks_encoder_input(dev, [ChunkTask(0, 300_000, 0, 0)])
+
+
+def _pcm16(x):
+    return np.clip(np.round(x.astype(np.float64) * 32767.0), -32768, 32767).astype(np.int16)
+
+
+def test_pcm16_chunks_equal_f32_of_decoded(extractor):
+    """16-bit PCM decoded in the kernel gives bit-identical features to the
+    f32 path over the reference's decode (value as f32 / 32767.0)."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: pcm16 long form")
+    pcm = _pcm16(synth.speech_like(1_500_000, 23))
+    dec = pcm.astype(np.float32) / np.float32(32767.0)
+    tasks = build_fast_execution_plan(pcm.size)
+    a, fa = extractor.extract_chunks(torch.from_numpy(dec).cuda(), tasks)
+    b, fb = extractor.extract_chunks_pcm(torch.from_numpy(pcm).cuda(), tasks)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)
+
+
+def test_pcm24_in_int32_equals_f32_of_decoded(extractor):
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: pcm24 in int32")
+    x = synth.speech_like(700_000, 29).astype(np.float64)
+    pcm = np.clip(np.round(x * 8388607.0), -8388608, 8388607).astype(np.int32)
+    dec = pcm.astype(np.float32) / np.float32(8388607.0)
+    tasks = build_fast_execution_plan(pcm.size)
+    a, _ = extractor.extract_chunks(torch.from_numpy(dec).cuda(), tasks)
+    b, _ = extractor.extract_chunks_pcm(torch.from_numpy(pcm).cuda(), tasks, bits_per_sample=24)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_pcm16_streamed_equals_resident(extractor):
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: pcm16 streamed")
+    pcm = _pcm16(synth.speech_like(3_000_000, 31))
+    tasks = build_fast_execution_plan(pcm.size)
+    a, fa = extractor.extract_chunks_pcm(torch.from_numpy(pcm).cuda(), tasks)
+    b, fb = extractor.extract_chunks_streamed(pcm, tasks, window_samples=960_000)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)
