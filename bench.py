@@ -1,17 +1,21 @@
 """Benchmark of the MI355X log-mel front end (one JSON line on stdout).
 
-A step is one pass of the front end over one batch of synthetic input that
-is already resident in HBM: the log-mel kernel, then the normalisation
-kernel, over every chunk of the workload.  The default workload is the
-1-hour long-form recording: 57.6M samples split into
-280 overlapping chunk tasks by scriptrs' planner, all featurized in one
-launch sequence.  The north-star bandwidth target is stated on this config.
+A step is one pass of the front end over one batch of synthetic input: the
+log-mel kernel, then the normalisation kernel, over every chunk of the
+workload.  The default workload is the 1-hour long-form recording (BASELINE
+config 3): 57.6M samples split into 280 overlapping chunk tasks by scriptrs'
+planner, all featurized in one launch sequence with the input already
+resident in HBM.  The north-star bandwidth target is stated on this config.
+Other workloads: config1/2/4 (resident), config5 (8 h streamed from pinned
+host memory in 60 s windows: PCIe-inclusive, never the headline figure).
+--pcm i16 feeds 16-bit PCM decoded in the kernel.
 
 value      = audio seconds featurized per second (RTFx), whole job
 roofline   = the log-mel kernel's algorithmic HBM bytes per launch
-             (4 B per unique input sample + 512 B per output frame) divided
+             (input bytes per unique sample + 512 B per output frame) divided
              by its mean duration (HIP events on the stream it runs on),
-             against the 8 TB/s HBM peak
+             against the 8 TB/s HBM peak; traffic = HBM bytes per launch from
+             the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
 cpu_baseline = the CPU oracle (C restatement of src/frontend.rs), timed on
              this host with 4 worker threads (the reference's default
              LongFormConfig::worker_count), over the whole workload
@@ -46,6 +50,10 @@ def make_workload(name: str):
     if name == "config3":
         x = synth.speech_like(57_600_000, 3)
         return x, build_fast_execution_plan(x.size), "1 h long-form recording, 280 overlap chunks, one batched pass"
+    if name == "config5":
+        x = synth.speech_like(460_800_000, 5)
+        return x, build_fast_execution_plan(x.size), \
+            "8 h recording streamed from pinned host memory in 60 s double-buffered windows"
     if name == "config4":
         x, off = synth.ragged_batch(256, 4)
         return x, [ChunkTask(int(off[i]), int(off[i + 1]), int(off[i]), 0) for i in range(256)], \
@@ -58,7 +66,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="config3", choices=["config1", "config2", "config3", "config4"])
+    ap.add_argument("--workload", default="config3", choices=["config1", "config2", "config3", "config4", "config5"])
+    ap.add_argument("--pcm", default="f32", choices=["f32", "i16"],
+                    help="input samples: f32, or 16-bit PCM decoded in the kernel")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -88,13 +98,30 @@ def main() -> int:
     print(f"[bench] workload {args.workload}: {desc}; N_audio={n_audio} tasks={len(tasks)} F_out={F}",
           file=sys.stderr, flush=True)
 
-    dev = torch.from_numpy(x).cuda()
     ext = ParakeetFeatureExtractor()
     out_dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
     out = torch.empty(F * 128, dtype=out_dt, device="cuda")
     stream = torch.cuda.current_stream()
+    if args.pcm == "i16":
+        x = np.clip(np.round(x.astype(np.float64) * 32767.0), -32768, 32767).astype(np.int16)
+    in_bytes = x.itemsize
+    streamed = args.workload == "config5"
+    if streamed:
+        # a new pinned host tensor (page-locked at allocation)
+        host = torch.from_numpy(x).pin_memory().numpy()
+
+        def step():
+            ext.extract_chunks_streamed(host, tasks, window_samples=960_000, dtype=args.dtype, out=out)
+    else:
+        dev = torch.from_numpy(x).cuda()
+
+        def step():
+            if args.pcm == "i16":
+                ext.extract_chunks_pcm(dev, tasks, dtype=args.dtype, stream=stream, out=out)
+            else:
+                ext.extract_chunks(dev, tasks, dtype=args.dtype, stream=stream, out=out)
     for _ in range(args.warmup):
-        ext.extract_chunks(dev, tasks, dtype=args.dtype, stream=stream, out=out)
+        step()
     torch.cuda.synchronize()
 
     L = _lib.lib()
@@ -103,7 +130,7 @@ def main() -> int:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        ext.extract_chunks(dev, tasks, dtype=args.dtype, stream=stream, out=out)
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     lm, nm, nl = ctypes.c_double(), ctypes.c_double(), ctypes.c_int32()
@@ -116,13 +143,13 @@ def main() -> int:
     logmel_ms = lm.value / args.steps
     norm_ms = nm.value / args.steps
     out_bytes = 4 if args.dtype == "f32" else 2
-    alg_logmel = 4 * n_audio + 512 * F                  # read audio once, write raw f32 log-mel
-    alg_path = 4 * n_audio + 128 * out_bytes * F        # the whole front end
+    alg_logmel = in_bytes * n_audio + 512 * F           # read audio once, write raw f32 log-mel
+    alg_path = in_bytes * n_audio + 128 * out_bytes * F  # the whole front end
     achieved = alg_logmel / (logmel_ms * 1e-3) / 1e9
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "sfe_logmel_longform_1h_traffic.json")
-    if args.workload == "config3" and os.path.exists(tfile):
+    if args.workload == "config3" and args.pcm == "f32" and os.path.exists(tfile):
         # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs
         # (scaled by a plain copy's counters); only valid for the kernel
         # source those runs measured.
@@ -146,21 +173,25 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded, scriptrs_amd/synth.py)",
         "config": {"workload": f"{args.workload}: {desc}", "n_audio_samples": n_audio, "chunks": len(tasks),
-                   "frames_out": F, "out_dtype": args.dtype},
+                   "frames_out": F, "out_dtype": args.dtype, "input": args.pcm,
+                   "input_location": "pinned host memory (PCIe-inclusive)" if streamed else "HBM"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "sfe_logmel_kernel",
                      "kernel_ms": logmel_ms, "alg_bytes": alg_logmel},
         "kernels_ms": {"sfe_logmel_kernel": logmel_ms, "sfe_norm_kernel": norm_ms},
         "path_gbps": alg_path / sec / 1e9,
     }
+    if streamed:
+        result["h2d_gbps"] = in_bytes * n_audio / sec / 1e9
 
-    if not args.no_cpu:
+    if not args.no_cpu and not streamed:
         import oracle
         starts = [t.audio_start for t in tasks]
         lens = [t.audio_end - t.audio_start for t in tasks]
-        oracle.extract_spans(x[:400_000], [0], [240_000], 1)  # load + warm
+        oracle.extract_spans(np.zeros(400_000, np.float32), [0], [240_000], 1)  # load + warm
         c0 = time.perf_counter()
-        want, _ = oracle.extract_spans(x, starts, lens, 4)
+        xf = x if x.dtype == np.float32 else x.astype(np.float32) / np.float32(32767.0)
+        want, _ = oracle.extract_spans(xf, starts, lens, 4)
         c1 = time.perf_counter()
         got = out.float().cpu().numpy()
         err = np.abs(got - want)

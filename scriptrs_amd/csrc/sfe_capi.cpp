@@ -31,6 +31,8 @@ struct Source {
 // Batching of one launch (see launch_pair).
 constexpr int kMaxBatches = 1;  // batching measured slower (see launch_pair); kept off
 constexpr int kMinUnitsPerBatch = 4096;  // 16-frame units; smaller calls run unbatched
+// Streamed extraction normalises after every this many windows.
+constexpr size_t kStreamNormWindows = 32;
 
 thread_local std::string g_last_error;
 
@@ -206,13 +208,18 @@ hipEvent_t sync_event(sfe_ctx* ctx, size_t i) {
 // fit on a CU together.  Events order each normalisation after its batch's
 // log-mel and join the aux stream back into `stream` at the end.  With
 // timing on, every kernel is bracketed by events (read by sfe_get_timing).
+//
+// stages selects the kernels: kLogmel, kNorm or both (kBoth; only then may
+// the call be batched).
+enum Stages { kLogmel = 1, kNorm = 2, kBoth = 3 };
+
 int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d_items, int n, float* raw,
-                void* out, int32_t out_dtype, int pad_to, hipStream_t stream) {
+                void* out, int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth) {
   if (n <= 0) return SFE_OK;
   const int u0 = items[0].tile_off;
   const int u1 = items[n - 1].tile_off + (int)sfe::tiles_for(items[n - 1].T);
   int nb = 1;
-  if (u1 - u0 >= kMinUnitsPerBatch * kMaxBatches) nb = std::min(kMaxBatches, n);
+  if (stages == kBoth && u1 - u0 >= kMinUnitsPerBatch * kMaxBatches) nb = std::min(kMaxBatches, n);
   const bool bf16 = out_dtype == SFE_BF16;
   if (nb > 1) {
     hipEvent_t fork = sync_event(ctx, 0);
@@ -241,9 +248,9 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* 
       for (int i = 0; i < 4; ++i)
         if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
     if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
-    SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_items + first, cnt, bu0, bu1 - bu0, ctx->d_tables,
-                               ctx->cfg.preemphasis, raw,
-                               ctx->grid_cap, stream));
+    if (stages & kLogmel)
+      SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_items + first, cnt, bu0, bu1 - bu0, ctx->d_tables,
+                                 ctx->cfg.preemphasis, raw, ctx->grid_cap, stream));
     if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
     if (nb > 1) {
       hipEvent_t done = sync_event(ctx, 1 + b);
@@ -252,7 +259,7 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* 
       SFE_HIP(hipStreamWaitEvent(ns, done, 0));
     }
     if (e[2]) SFE_HIP(hipEventRecord(e[2], ns));
-    SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, pad_to, out, bf16, nb > 1, ns));
+    if (stages & kNorm) SFE_HIP(sfe::launch_norm(raw, d_items + first, cnt, max_T, pad_to, out, bf16, nb > 1, ns));
     if (e[3]) SFE_HIP(hipEventRecord(e[3], ns));
     first = last;
   }
@@ -640,9 +647,18 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
   SFE_HIP(ctx->meta.reserve(mbytes));
   SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
+  // A recording already in pinned (page-locked) host memory is copied to
+  // the device directly; pageable memory goes through two pinned staging
+  // windows.
+  bool pinned = false;
+  {
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, host_recording) == hipSuccess) pinned = attr.type == hipMemoryTypeHost;
+    (void)hipGetLastError();  // a pageable pointer leaves an error code behind
+  }
   for (int b = 0; b < 2; ++b) {
     SFE_HIP(ctx->win[b].reserve((size_t)window_samples * es));
-    SFE_HIP(ctx->h_win[b].reserve((size_t)window_samples * es));
+    if (!pinned) SFE_HIP(ctx->h_win[b].reserve((size_t)window_samples * es));
   }
   hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
   memcpy(ctx->h_meta.ptr, items.data(), mbytes);
@@ -651,26 +667,43 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
   ctx->h_meta.pending = true;
   const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
   bool used[2] = {false, false};
+  int32_t norm_first = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
     const Group& g = groups[gi];
     const int b = (int)(gi & 1);
     const size_t bytes = (size_t)(g.wend - g.wstart) * es;
-    // the pinned buffer is free once its previous H2D copy has finished
-    SFE_HIP(ctx->h_win[b].wait());
-    memcpy(ctx->h_win[b].ptr, host + (size_t)g.wstart * es, bytes);
+    const void* hsrc = host + (size_t)g.wstart * es;
+    if (!pinned) {
+      // the pinned staging buffer is free once its previous H2D copy has finished
+      SFE_HIP(ctx->h_win[b].wait());
+      memcpy(ctx->h_win[b].ptr, hsrc, bytes);
+      hsrc = ctx->h_win[b].ptr;
+    }
     // the device window is free once the kernels that read it have finished
     if (used[b]) SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_done[b], 0));
-    SFE_HIP(hipMemcpyAsync(ctx->win[b].ptr, ctx->h_win[b].ptr, bytes, hipMemcpyHostToDevice, sx));
-    SFE_HIP(hipEventRecord(ctx->h_win[b].ev, sx));
-    ctx->h_win[b].pending = true;
+    SFE_HIP(hipMemcpyAsync(ctx->win[b].ptr, hsrc, bytes, hipMemcpyHostToDevice, sx));
+    if (!pinned) {
+      SFE_HIP(hipEventRecord(ctx->h_win[b].ev, sx));
+      ctx->h_win[b].pending = true;
+    }
     SFE_HIP(hipEventRecord(ctx->ev_copied[b], sx));
     SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[b], 0));
     Source wsrc = src;
     wsrc.ptr = ctx->win[b].ptr;
-    rc = launch_pair(ctx, wsrc, items.data() + g.first, d_items + g.first, g.count,
-                     raw, out, out_dtype, 0, sc);
+    rc = launch_pair(ctx, wsrc, items.data() + g.first, d_items + g.first, g.count, raw, out, out_dtype, 0, sc,
+                     kLogmel);
     if (rc) return rc;
     SFE_HIP(hipEventRecord(ctx->ev_done[b], sc));
+    // Normalisation reads only the raw log-mel (all of it stays in HBM), so
+    // it runs once per kStreamNormWindows windows instead of per window:
+    // one launch over many items instead of many launches over a few.
+    const int32_t norm_end = g.first + g.count;
+    if (gi + 1 == groups.size() || (gi + 1) % kStreamNormWindows == 0) {
+      rc = launch_pair(ctx, wsrc, items.data() + norm_first, d_items + norm_first, norm_end - norm_first, raw, out,
+                       out_dtype, 0, sc, kNorm);
+      if (rc) return rc;
+      norm_first = norm_end;
+    }
     used[b] = true;
   }
   SFE_HIP(hipStreamSynchronize(sc));
