@@ -6,7 +6,7 @@ All feature computation runs in hand-written gfx950 HIP kernels inside
 """
 from .frontend import (  # noqa: F401
     AudioTooLong, ChunkPreparer, EmptyAudio, InvalidModelOutput, ParakeetFeatureExtractor, PreparedChunk,
-    TranscriptionConfig, TranscriptionError, build_tables, num_frames,
+    TaskTable, TranscriptionConfig, TranscriptionError, build_tables, num_frames,
 )
 from .long_form import (  # noqa: F401
     ChunkTask, LongFormConfig, LongFormFeatures, OverlapChunkConfig, SampleRange, build_fast_execution_plan,

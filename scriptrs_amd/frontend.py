@@ -195,9 +195,9 @@ class ParakeetFeatureExtractor:
         copying the overlaps (replaces the per-task ``ChunkPreparer::prepare``
         calls of src/long_form.rs:584-592)."""
         import torch
-        arr, n = _tasks_array(tasks)
-        fo = np.zeros(n + 1, np.int64)
-        fo[1:] = np.cumsum([(t.audio_end - t.audio_start) // self.config.hop_length + 1 for t in arr])
+        tt = _tasks_array(tasks, self.config.hop_length)
+        arr, n = tt.ptr, tt.n
+        fo = tt.frame_offsets.copy()
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
             out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=recording.device)
@@ -215,9 +215,9 @@ class ParakeetFeatureExtractor:
         the container width."""
         import torch
         pcm, bits = _pcm_format(recording.dtype, bits_per_sample)
-        arr, n = _tasks_array(tasks)
-        fo = np.zeros(n + 1, np.int64)
-        fo[1:] = np.cumsum([(t.audio_end - t.audio_start) // self.config.hop_length + 1 for t in arr])
+        tt = _tasks_array(tasks, self.config.hop_length)
+        arr, n = tt.ptr, tt.n
+        fo = tt.frame_offsets.copy()
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
             out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=recording.device)
@@ -235,7 +235,8 @@ class ParakeetFeatureExtractor:
         to ``max_feature_frames()`` (``PreparedChunk::target_frames``,
         src/pipeline.rs:160-163).  Returns ``(out, feature_frames)``."""
         import torch
-        arr, n = _tasks_array(tasks)
+        tt = _tasks_array(tasks, self.config.hop_length)
+        arr, n = tt.ptr, tt.n
         tf = int(target_frames or self.config.max_feature_frames())
         ff = np.zeros(n, np.int64)
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
@@ -257,9 +258,9 @@ class ParakeetFeatureExtractor:
         if h.dtype not in (np.float32, np.int16, np.int32):
             h = h.astype(np.float32)
         pcm, bits = _pcm_format(h.dtype, bits_per_sample)
-        arr, n = _tasks_array(tasks)
-        fo = np.zeros(n + 1, np.int64)
-        fo[1:] = np.cumsum([(t.audio_end - t.audio_start) // self.config.hop_length + 1 for t in arr])
+        tt = _tasks_array(tasks, self.config.hop_length)
+        arr, n = tt.ptr, tt.n
+        fo = tt.frame_offsets.copy()
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
             out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=f"cuda:{self.device}")
@@ -290,14 +291,32 @@ def _dtype_code(dtype: str) -> int:
     raise InvalidModelOutput(f"unsupported dtype {dtype!r}")
 
 
-def _tasks_array(tasks):
-    n = len(tasks)
-    if n == 0:
-        raise InvalidModelOutput("no tasks")
-    arr = (SfeChunk * n)()
-    for i, t in enumerate(tasks):
-        arr[i] = SfeChunk(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples)
-    return arr, n
+class TaskTable:
+    """Chunk tasks in the C ABI's ``sfe_chunk`` layout (4 x int64 per task:
+    audio_start, audio_end, global_sample_offset, context_samples) with their
+    frame offsets.  Build it once per plan and pass it to the ``extract_chunks*``
+    calls; a plain list of ``ChunkTask`` is converted on every call."""
+
+    def __init__(self, tasks, hop_length: int = 160):
+        if isinstance(tasks, np.ndarray):
+            a = np.ascontiguousarray(tasks, np.int64).reshape(-1, 4)
+        else:
+            a = np.array([(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples) for t in tasks],
+                         np.int64).reshape(-1, 4)
+        if a.shape[0] == 0:
+            raise InvalidModelOutput("no tasks")
+        self.array = a
+        self.n = int(a.shape[0])
+        self.frame_offsets = np.zeros(self.n + 1, np.int64)
+        np.cumsum((a[:, 1] - a[:, 0]) // hop_length + 1, out=self.frame_offsets[1:])
+        self.ptr = a.ctypes.data_as(ctypes.POINTER(SfeChunk))
+
+    def __len__(self):
+        return self.n
+
+
+def _tasks_array(tasks, hop_length: int = 160) -> TaskTable:
+    return tasks if isinstance(tasks, TaskTable) else TaskTable(tasks, hop_length)
 
 
 @dataclass

@@ -229,3 +229,32 @@ def test_pcm16_streamed_equals_resident(extractor):
     torch.cuda.synchronize()
     assert np.array_equal(fa, fb)
     assert torch.equal(a, b)
+
+
+def test_calls_on_two_streams_and_repeated_plans(extractor):
+    """Back-to-back calls on different streams share the context's item table
+    and raw scratch: the second call is ordered after the first on the GPU.
+    A repeated plan reuses the uploaded item table and gives identical output."""
+    import torch
+    from scriptrs_amd import TaskTable, build_fast_execution_plan
+    _flush("case: two streams, repeated plan")
+    ra = synth.speech_like(1_200_000, 41)
+    rb = synth.speech_like(900_000, 43)
+    ta = TaskTable(build_fast_execution_plan(ra.size))
+    tb = TaskTable(build_fast_execution_plan(rb.size))
+    da, db = torch.from_numpy(ra).cuda(), torch.from_numpy(rb).cuda()
+    want_a, _ = extractor.extract_chunks(da, ta)
+    want_b, _ = extractor.extract_chunks(db, tb)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for _ in range(3):
+        oa, _ = extractor.extract_chunks(da, ta, stream=s1)
+        ob, _ = extractor.extract_chunks(db, tb, stream=s2)
+        oa2, _ = extractor.extract_chunks(da, ta, stream=s2)
+        outs.append((oa, ob, oa2))
+    torch.cuda.synchronize()
+    for oa, ob, oa2 in outs:
+        assert torch.equal(oa, want_a)
+        assert torch.equal(ob, want_b)
+        assert torch.equal(oa2, want_a)
