@@ -793,11 +793,16 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   if constexpr (N > 0) {
     if (T <= kSpan * N) {
       float4 v[N];
+      // Unconditional loads from an in-bounds frame (rounds past the item
+      // reread the lane's first frame), selected afterwards: a load under a
+      // branch waits for itself, and the rounds would load one at a time.
 #pragma unroll
       for (int j = 0; j < N; ++j) {
-        v[j] = x0;  // padding with x0 keeps the constancy test exact
-        if (j < nr) v[j] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
+        const size_t off = j < nr ? (size_t)j * (kSpan * kMel) + lo : (size_t)lo;
+        v[j] = *reinterpret_cast<const float4*>(xb + (nr > 0 ? off : (size_t)(4 * q)));
       }
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = j < nr ? ln2_scale(v[j]) : x0;  // x0 padding keeps the constancy test exact
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         float a = 0.0f;
@@ -850,8 +855,10 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   for (int j0 = 0; j0 < nr; j0 += G) {
     float4 e[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-      if (j0 + g < nr) e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo));
+    for (int g = 0; g < G; ++g) {
+      const int j = j0 + g < nr ? j0 + g : j0;  // in bounds; unused when past the item
+      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float a = 0.0f;
@@ -873,8 +880,10 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   for (int j0 = 0; j0 < nr; j0 += G) {
     float4 e[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-      if (j0 + g < nr) e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)(j0 + g) * (kSpan * kMel) + lo));
+    for (int g = 0; g < G; ++g) {
+      const int j = j0 + g < nr ? j0 + g : j0;  // in bounds; unused when past the item
+      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float a = 0.0f;
@@ -893,8 +902,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     float4 e[4];
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr) {
+      // past the item: the item's first frame (always in bounds), unused
       const int j = 4 * ch + jr;
-      if (j < nr) e[jr] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
+      e[jr] = ln2_scale(*reinterpret_cast<const float4*>(xb + (j < nr ? (size_t)j * (kSpan * kMel) + lo : (size_t)(4 * q))));
     }
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr)
