@@ -258,3 +258,82 @@ def test_calls_on_two_streams_and_repeated_plans(extractor):
         assert torch.equal(oa, want_a)
         assert torch.equal(ob, want_b)
         assert torch.equal(oa2, want_a)
+
+
+@pytest.mark.parametrize("n", [327_680, 327_840, 480_000])
+def test_items_longer_than_register_budget(extractor, n):
+    """T > 2048 frames takes the normalisation kernel's streaming path
+    (327,680 samples -> T = 2049; 480,000 -> T = 3001)."""
+    _flush(f"case: long item {n}")
+    a = synth.sinusoids(n, 300 + n % 97)
+    got = extractor.extract(a)
+    want = oracle.extract(a).T
+    assert got.shape == (n // 160 + 1, 128)
+    assert_parity(got, want, R.extract(a).T, R.f32_noise_envelope(a).T, what=f"len {n}")
+
+
+def test_config2_full_dense_batch(extractor):
+    """BASELINE config 2 at full size: 64 x 15 s clips in one call; frame
+    counts exact, every clip's rows normalised (mean ~ 0 as the reference's
+    own test, src/frontend.rs:292-300), eight clips checked element-wise."""
+    import torch
+    _flush("case: config 2 full")
+    x = synth.dense_batch(64, 240_000, 1000)
+    dev = torch.from_numpy(x.reshape(-1)).cuda()
+    off = np.arange(65, dtype=np.int64) * 240_000
+    out, fo = extractor.extract_batch(dev, off)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    assert list(np.diff(fo)) == [1501] * 64
+    feats = out.reshape(64, 128, 1501)
+    assert np.abs(feats.mean(axis=2)).max() < 1e-4
+    for i in (0, 9, 21, 32, 40, 51, 62, 63):
+        assert_parity(feats[i], oracle.extract(x[i]), R.extract(x[i]), R.f32_noise_envelope(x[i]), what=f"clip {i}")
+
+
+def test_config4_full_ragged_batch(extractor):
+    """BASELINE config 4 at full size: 256 clips of 1-20 s in one flat buffer;
+    frame counts exact against the oracle, all clips against the f32 oracle
+    at the plain bar except elements near the guard (the f32 FFT noise the
+    envelope models), twelve clips checked with the full bound."""
+    import torch
+    _flush("case: config 4 full")
+    flat, off = synth.ragged_batch(256, 4)
+    dev = torch.from_numpy(flat).cuda()
+    out, fo = extractor.extract_batch(dev, off)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    want, wfo = oracle.extract_spans(flat, off[:-1], np.diff(off), 4)
+    assert np.array_equal(fo, wfo)
+    err = np.abs(out - want)
+    assert np.mean(err <= 1e-4 + 1e-3 * np.abs(want)) > 0.999
+    for i in (0, 1, 17, 64, 100, 127, 128, 150, 200, 222, 254, 255):
+        a = flat[off[i]:off[i + 1]]
+        got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert_parity(got, want[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1), R.extract(a), R.f32_noise_envelope(a),
+                      what=f"clip {i}")
+
+
+def test_config3_full_invariants(extractor):
+    """BASELINE config 3 at full size (57.6M samples, 280 chunk tasks): frame
+    offsets exact, each chunk's rows normalised (mean ~ 0, the reference's
+    invariant, src/frontend.rs:292-300), and the first, a middle and the last
+    chunk element-wise against the oracle."""
+    import torch
+    from scriptrs_amd import TaskTable, build_fast_execution_plan
+    _flush("case: config 3 full")
+    rec = synth.speech_like(57_600_000, 3)
+    tasks = TaskTable(build_fast_execution_plan(rec.size))
+    assert tasks.n == 280 and tasks.frame_offsets[-1] == 418_312
+    out, fo = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+    torch.cuda.synchronize()
+    assert np.array_equal(fo, tasks.frame_offsets)
+    out = out.cpu().numpy()
+    for i in range(tasks.n):
+        rows = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert np.abs(rows.mean(axis=1)).max() < 1e-4, i
+    for i in (0, 140, 279):
+        s, e = int(tasks.array[i, 0]), int(tasks.array[i, 1])
+        a = rec[s:e]
+        got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
