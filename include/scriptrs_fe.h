@@ -186,6 +186,25 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
                               int32_t target_frames, int32_t out_dtype, void* out, int64_t* feature_frames,
                               void* stream);
 
+/* Silero VAD model inputs.  Replaces the framing half of the reference's
+ * VAD loop (process_coreml_vad, src/long_form/vad.rs:62-99; window 512 and
+ * context 64 samples, src/constants.rs:6-11): for each 512-sample window w
+ * of the recording, the 576 floats the model is fed, [64 context | 512
+ * window].  The first context is zeros; later contexts are the previous
+ * window's last 64 samples; a short last window repeats its last sample
+ * (vad.rs:81-84).  sfe_vad_num_windows(len) = ceil(len / 512) rows. */
+int64_t sfe_vad_num_windows(int64_t len);
+
+/* Writes sfe_vad_num_windows(len) rows of 576 f32 to out (device memory,
+ * 16-byte aligned, room for out_windows rows), row-major [n][576].  The
+ * recording is a device buffer in PCM format `pcm_format` (sfe_pcm), decoded
+ * as in sfe_extract_chunks_pcm.  len == 0 writes nothing and returns SFE_OK
+ * (the reference returns an empty probability list for empty audio,
+ * vad.rs:67-69).  Asynchronous on `stream`; ordered after the context's
+ * earlier calls. */
+int sfe_vad_frames(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample, int64_t len,
+                   float* out, int64_t out_windows, void* stream);
+
 /* Streaming long-form extraction from HOST memory.  The recording is
  * copied host->device in windows of at most window_samples samples,
  * double-buffered on two streams: the copy of window w+1 overlaps the

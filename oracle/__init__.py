@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
         L.sfo_stft_power.restype = ctypes.c_int
         L.sfo_extract_spans.argtypes = [f32p, i64p, i64p, i32, f32p, i64p, i32]
         L.sfo_extract_spans.restype = ctypes.c_int
+        L.sfo_vad_frames.argtypes = [f32p, i64, f32p]
+        L.sfo_vad_frames.restype = i64
         _lib = L
     return _lib
 
@@ -130,3 +132,14 @@ def extract_spans(samples: np.ndarray, starts, lens, nthreads: int = 4):
     if rc != 0:
         raise ValueError("EmptyAudio")
     return out, fo
+
+
+def vad_frames(audio: np.ndarray) -> np.ndarray:
+    """Silero VAD model inputs, [ceil(len/512), 576] float32: the reference's
+    window/context loop (``src/long_form/vad.rs:62-99``) restated in C."""
+    a = np.ascontiguousarray(audio, np.float32).reshape(-1)
+    n = (a.size + 511) // 512
+    out = np.empty((n, 576), np.float32)
+    rows = lib().sfo_vad_frames(_fp(a), a.size, _fp(out))
+    assert rows == n
+    return out

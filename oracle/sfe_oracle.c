@@ -344,3 +344,33 @@ int sfo_extract_spans(const float* samples, const int64_t* starts, const int64_t
   tables_free(&t);
   return job.status;
 }
+
+/* Silero VAD model inputs, restated as the reference's loop
+ * (process_coreml_vad, src/long_form/vad.rs:62-99; window 512, context 64,
+ * src/constants.rs:6-11): per window, copy the chunk, pad a short one with
+ * its last sample, emit [context | chunk], then keep the chunk's last 64
+ * samples as the next context.  out: ceil(len/512) rows of 576 floats.
+ * Returns the number of rows. */
+int64_t sfo_vad_frames(const float* audio, int64_t len, float* out) {
+  enum { WIN = 512, CTX = 64 };
+  float context[CTX];
+  float chunk[WIN];
+  memset(context, 0, sizeof(context));
+  memset(chunk, 0, sizeof(chunk));
+  int64_t rows = 0;
+  for (int64_t start = 0; start < len; start += WIN) {
+    const int64_t end = start + WIN < len ? start + WIN : len;
+    const int64_t n = end - start;
+    memcpy(chunk, audio + start, (size_t)n * sizeof(float));
+    if (n < WIN) {
+      const float last = chunk[n > 0 ? n - 1 : 0];
+      for (int64_t k = n; k < WIN; ++k) chunk[k] = last;
+    }
+    float* row = out + rows * (WIN + CTX);
+    memcpy(row, context, sizeof(context));
+    memcpy(row + CTX, chunk, sizeof(chunk));
+    memcpy(context, chunk + (WIN - CTX), sizeof(context));
+    ++rows;
+  }
+  return rows;
+}

@@ -12,3 +12,6 @@ from .long_form import (  # noqa: F401
     ChunkTask, LongFormConfig, LongFormFeatures, OverlapChunkConfig, SampleRange, build_fast_execution_plan,
     featurize_long_form, parallel_worker_count,
 )
+from .vad import (  # noqa: F401
+    VAD_CONTEXT_SAMPLES, VAD_INPUT_SAMPLES, VAD_WINDOW_SAMPLES, SileroVadFramer, vad_num_windows,
+)

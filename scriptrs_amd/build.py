@@ -29,6 +29,7 @@ COMMON = [
 SOURCES = [
     # (source, extra flags)
     ("sfe_kernels.hip", ["-x", "hip"]),
+    ("sfe_vad.hip", ["-x", "hip"]),
     # bit-exact table construction: every f32/f64 op rounded separately
     ("sfe_tables.cpp", ["-x", "hip", "-ffp-contract=off"]),
     ("sfe_capi.cpp", ["-x", "hip"]),

@@ -604,6 +604,33 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
                    target_frames);
 }
 
+int64_t sfe_vad_num_windows(int64_t len) { return sfe::vad_num_windows(len); }
+
+int sfe_vad_frames(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample, int64_t len,
+                   float* out, int64_t out_windows, void* stream) {
+  if (len < 0) return fail(SFE_INVALID_ARG, "negative recording length");
+  Source src;
+  int rc = pcm_source(recording, pcm_format, bits_per_sample, &src);
+  if (rc) return rc;
+  const int64_t n = sfe::vad_num_windows(len);
+  if (n == 0) return SFE_OK;  // empty audio: no windows (src/long_form/vad.rs:67-69)
+  if (!recording || !out) return fail(SFE_INVALID_ARG, "null recording or output");
+  if (out_windows < n)
+    return fail(SFE_INVALID_ARG, "output holds " + std::to_string(out_windows) + " windows, " + std::to_string(n) +
+                                     " needed");
+  if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return fail(SFE_INVALID_ARG, "output must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(recording) % src.esize != 0)
+    return fail(SFE_INVALID_ARG, "recording is not aligned to its sample size");
+  if ((rc = check_ctx(ctx))) return rc;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(s, ctx->ev_last, 0));
+  SFE_HIP(sfe::launch_vad_frames(src.ptr, src.pcm, src.scale, len, out, s));
+  SFE_HIP(hipEventRecord(ctx->ev_last, s));
+  ctx->has_last = true;
+  return SFE_OK;
+}
+
 int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, const sfe_chunk* tasks, int32_t n,
                                 int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples) {
   return sfe_extract_chunks_streamed_pcm(ctx, host, SFE_PCM_F32, 32, len, tasks, n, out_dtype, out, frame_offsets,

@@ -92,4 +92,14 @@ constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: o
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, int pad_to, void* out,
                        bool out_bf16, bool lean, hipStream_t stream);
 
+// Silero VAD model inputs (sfe_vad.hip): [64 context | 512 window] f32 per
+// 512-sample window (src/long_form/vad.rs:62-99, src/constants.rs).
+constexpr int kVadWin = 512;
+constexpr int kVadCtx = 64;
+constexpr int kVadRow = kVadWin + kVadCtx;
+int64_t vad_num_windows(int64_t len);  // ceil(len / 512); 0 for len <= 0
+// Writes vad_num_windows(len) rows of kVadRow floats to out (16-byte aligned).
+hipError_t launch_vad_frames(const void* samples, int pcm, float pcm_scale, int64_t len, float* out,
+                             hipStream_t stream);
+
 }  // namespace sfe
