@@ -40,6 +40,20 @@ SR = 16_000
 HBM_PEAK_GBS = 8000.0
 
 
+def measured_traffic(fname: str, applies: bool):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (each scaled by what the counter reads for a plain copy),
+    or None.  Only valid for the kernel source those runs measured, whose
+    sha256 the file records."""
+    import hashlib
+    tfile = os.path.join(ROOT, "profiles", fname)
+    if not applies or not os.path.exists(tfile):
+        return None
+    t = json.load(open(tfile))
+    src = open(os.path.join(ROOT, t["kernel_source"]), "rb").read()
+    return t["traffic_bytes"] if hashlib.sha256(src).hexdigest() == t["kernel_source_sha256"] else None
+
+
 def make_workload(name: str):
     from scriptrs_amd import synth
     from scriptrs_amd.long_form import build_fast_execution_plan, ChunkTask
@@ -159,17 +173,7 @@ def main() -> int:
     alg_path = in_bytes * n_audio + 128 * out_bytes * F  # the whole front end
     achieved = alg_logmel / (logmel_ms * 1e-3) / 1e9
 
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", "sfe_logmel_longform_1h_traffic.json")
-    if args.workload == "config3" and args.pcm == "f32" and os.path.exists(tfile):
-        # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-        # (scaled by a plain copy's counters); only valid for the kernel
-        # source those runs measured.
-        import hashlib
-        t = json.load(open(tfile))
-        src = open(os.path.join(ROOT, t["kernel_source"]), "rb").read()
-        if hashlib.sha256(src).hexdigest() == t["kernel_source_sha256"]:
-            traffic = t["traffic_bytes"]
+    traffic = measured_traffic("sfe_logmel_longform_1h_traffic.json", args.workload == "config3" and args.pcm == "f32")
 
     result = {
         "metric": "audio-sec featurized/sec (RTFx) + achieved HBM GB/s vs peak, 1 MI355X",
@@ -270,7 +274,9 @@ def bench_vad(args) -> int:
         "config": {"workload": f"vad1h: {desc}", "n_audio_samples": n_audio, "windows": n_win,
                    "input": args.pcm, "input_location": "HBM"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "sfe_vad_frames_kernel",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": measured_traffic("sfe_vad_frames_1h_traffic.json", args.pcm == "f32"),
+                     "kernel": "sfe_vad_frames_kernel",
                      "kernel_ms": kernel_ms, "alg_bytes": alg},
         "kernels_ms": {"sfe_vad_frames_kernel": kernel_ms},
     }
