@@ -910,7 +910,7 @@ hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const It
                          hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
   const int grid = n_units < grid_cap ? n_units : grid_cap;
-  Decode dc{pcm_scale, 1.0f / pcm_scale};  // the host's division is correctly rounded
+  Decode dc{pcm_scale, 1.0f / pcm_scale, 1.0 / (double)pcm_scale};  // the host's divisions are correctly rounded
   const dim3 g(grid), b(kThreads);
   if (pcm == kPcmI16)
     sfe_logmel_kernel<int16_t><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items, unit0,

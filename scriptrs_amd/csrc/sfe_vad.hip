@@ -102,7 +102,7 @@ hipError_t launch_vad_frames(const void* samples, int pcm, float pcm_scale, int6
   const int64_t n = vad_num_windows(len);
   if (n == 0) return hipSuccess;
   const dim3 g((unsigned)((n + kVadRowsPerBlock - 1) / kVadRowsPerBlock)), b(kVadThreads);
-  const Decode dc{pcm_scale, 1.0f / pcm_scale};
+  const Decode dc{pcm_scale, 1.0f / pcm_scale, 1.0 / (double)pcm_scale};
   if (pcm == kPcmI16)
     sfe_vad_frames_kernel<int16_t><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), len, n, dc, out);
   else if (pcm == kPcmI32)

@@ -169,10 +169,10 @@ def _residual_div(v, scale, recip):
     return _rn32(Fraction(float(q)) + Fraction(float(e)) * Fraction(float(r)))
 
 
-def test_pcm_decode_is_correctly_rounded_for_every_int16():
-    """The in-kernel decode of 16-bit PCM equals the reference's f32 division
-    value as f32 / 32767.0 (examples/transcribe_wav.rs:342-348) for all
-    65536 inputs: the residual step reproduces IEEE division exactly."""
+def test_pcm_decode_is_correctly_rounded_for_every_int32_holding_16_bits():
+    """The int32-container decode (Markstein residual step) equals the
+    reference's f32 division value as f32 / 32767.0
+    (examples/transcribe_wav.rs:342-348) for all 65536 16-bit inputs."""
     scale = np.float32(32767.0)
     recip = np.float32(1.0) / scale
     v = np.arange(-32768, 32768, dtype=np.float32)
@@ -182,6 +182,21 @@ def test_pcm_decode_is_correctly_rounded_for_every_int16():
     todo = np.nonzero(q != want)[0]
     for i in todo:
         assert _residual_div(v[i], scale, recip) == want[i], int(v[i])
+
+
+@pytest.mark.parametrize("bits", range(2, 17))
+def test_int16_decode_is_correctly_rounded_for_every_value(bits):
+    """The int16-container decode RN_f32(RN_f64(v * RN_f64(1 / scale))) equals
+    correctly rounded f32 division for every int16 value at every width (a
+    plain f32 multiply by RN_f32(1 / scale) would not: it is wrong for
+    thousands of values at most widths)."""
+    scale = np.float32((1 << (bits - 1)) - 1)
+    v = np.arange(-32768, 32768, dtype=np.int64)
+    want = v.astype(np.float32) / scale
+    got = (v.astype(np.float64) * (1.0 / np.float64(scale))).astype(np.float32)
+    assert np.array_equal(got, want)
+    if bits > 2:
+        assert np.count_nonzero(v.astype(np.float32) * (np.float32(1.0) / scale) != want) > 0
 
 
 def test_pcm_decode_24_bit_sample():

@@ -204,6 +204,22 @@ def test_pcm16_chunks_equal_f32_of_decoded(extractor):
     assert torch.equal(a, b)
 
 
+def test_pcm12_in_int16_chunks_equal_f32_of_decoded(extractor):
+    """12-bit samples in int16 containers (scale 2047)."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: pcm12 in int16 long form")
+    x = synth.speech_like(600_000, 29)
+    pcm = np.clip(np.round(x * 2047.0), -2048, 2047).astype(np.int16)
+    dec = pcm.astype(np.float32) / np.float32(2047.0)
+    tasks = build_fast_execution_plan(pcm.size)
+    a, fa = extractor.extract_chunks(torch.from_numpy(dec).cuda(), tasks)
+    b, fb = extractor.extract_chunks_pcm(torch.from_numpy(pcm).cuda(), tasks, bits_per_sample=12)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)
+
+
 def test_pcm24_in_int32_equals_f32_of_decoded(extractor):
     import torch
     from scriptrs_amd import build_fast_execution_plan

@@ -61,6 +61,18 @@ def test_pcm16_equals_f32_of_decoded(framer):
     assert np.array_equal(got.cpu().numpy(), oracle.vad_frames(dec))
 
 
+def test_pcm12_in_int16_equals_f32_of_decoded(framer):
+    """12-bit samples in int16 containers (scale 2047), including values
+    outside the 12-bit range, which the reference's formula also divides."""
+    import torch
+    _flush("case: vad pcm12 in int16")
+    pcm = np.random.default_rng(44).integers(-32768, 32768, 300_001).astype(np.int16)
+    dec = pcm.astype(np.float32) / np.float32(2047.0)
+    got = framer.model_inputs(torch.from_numpy(pcm).cuda(), bits_per_sample=12)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.vad_frames(dec))
+
+
 def test_pcm24_in_int32_equals_f32_of_decoded(framer):
     import torch
     _flush("case: vad pcm24 in int32")
