@@ -86,6 +86,8 @@ def main() -> int:
     ap.add_argument("--pcm", default="f32", choices=["f32", "i16"],
                     help="input samples: f32, or 16-bit PCM decoded in the kernel")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16"])
+    ap.add_argument("--window-samples", type=int, default=960_000,
+                    help="config5: device window length in samples (60 s at 16 kHz by default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB per step (calibrates the HBM byte counters)")
@@ -130,7 +132,7 @@ def main() -> int:
         host = torch.from_numpy(x).pin_memory().numpy()
 
         def step():
-            ext.extract_chunks_streamed(host, tasks, window_samples=960_000, dtype=args.dtype, out=out)
+            ext.extract_chunks_streamed(host, tasks, window_samples=args.window_samples, dtype=args.dtype, out=out)
     else:
         dev = torch.from_numpy(x).cuda()
 
@@ -199,6 +201,7 @@ def main() -> int:
     }
     if streamed:
         result["h2d_gbps"] = in_bytes * n_audio / sec / 1e9
+        result["config"]["window_samples"] = args.window_samples
 
     if not args.no_cpu and not streamed:
         import oracle

@@ -205,14 +205,17 @@ int64_t sfe_vad_num_windows(int64_t len);
 int sfe_vad_frames(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample, int64_t len,
                    float* out, int64_t out_windows, void* stream);
 
-/* Streaming long-form extraction from HOST memory.  The recording is
- * copied host->device in windows of at most window_samples samples,
- * double-buffered on two streams: the copy of window w+1 overlaps the
- * compute of window w.  Each window carries every task that ends inside
- * it, plus its left halo.  `out` is a device buffer sized as for
- * sfe_extract_chunks.  Copies stage through pinned buffers, so `host`
- * may be pageable.  Synchronous: returns after all work completes.
- * window_samples must be at least the longest task. */
+/* Streaming long-form extraction from HOST memory.  Tasks are grouped
+ * into windows of at most window_samples samples; each window carries every
+ * task that ends inside it, plus its left halo.  Consecutive windows form
+ * batches of about 64 MB (1 to 64 windows), each copied host->device as one
+ * contiguous range and featurized by one launch, double-buffered on two
+ * streams: the copy of batch b+1 overlaps the compute of batch b.  Device
+ * memory for the copies: two batches.  `out` is a device buffer sized as for
+ * sfe_extract_chunks.  A pinned (page-locked) `host` buffer is copied
+ * directly; a pageable one is staged through pinned buffers.  Synchronous:
+ * returns after all work completes.  window_samples must be at least the
+ * longest task, and tasks must be ordered by audio_start. */
 int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host_recording, int64_t len, const sfe_chunk* tasks,
                                 int32_t n, int32_t out_dtype, void* out, int64_t* frame_offsets,
                                 int64_t window_samples);

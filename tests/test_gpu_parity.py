@@ -122,6 +122,42 @@ def test_streamed_equals_resident(extractor):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("pinned", [False, True])
+def test_streamed_ring_wraps_equals_resident(extractor, pinned):
+    """One task per window (250,000-sample windows) over 12 M samples: about
+    58 windows, so the device ring of window slots wraps many times and the
+    normalisation runs at its 32-window boundary and at the end."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush(f"case: streamed ring wrap pinned={pinned}")
+    rec = synth.speech_like(12_000_000, 19)
+    host = torch.from_numpy(rec).pin_memory().numpy() if pinned else rec
+    tasks = build_fast_execution_plan(rec.size)
+    assert len(tasks) > 40
+    a, fa = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+    b, fb = extractor.extract_chunks_streamed(host, tasks, window_samples=250_000)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("window", [250_000, 960_000])
+def test_streamed_sparse_tasks_equal_resident(extractor, window):
+    """Every third chunk task only (a plan with gaps, as speech regions
+    give): batches of windows must not copy past their device half, and
+    gaps larger than a window split batches."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush(f"case: streamed sparse tasks window={window}")
+    rec = synth.speech_like(12_000_000, 21)
+    tasks = build_fast_execution_plan(rec.size)[::3]
+    a, fa = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+    b, fb = extractor.extract_chunks_streamed(rec, tasks, window_samples=window)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)
+
+
 def test_long_form_batched_pipeline(extractor):
     """A call large enough to run as several log-mel batches with the lean
     normalisation overlapping on the aux stream: frame offsets exact for every
