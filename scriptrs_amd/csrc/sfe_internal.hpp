@@ -86,11 +86,10 @@ constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: o
 // Normalises raw (f32 log2 values, frame-major [T][128] per item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
-// frame count (sizes the kernel's register budget).  lean selects the
-// low-footprint variant that co-runs with the log-mel kernel.  pad_to > 0:
-// rows of pad_to frames, zero past T (the encoder input layout).
+// frame count (sizes the kernel's register budget).  pad_to > 0: rows of
+// pad_to frames, zero past T (the encoder input layout).
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, int pad_to, void* out,
-                       bool out_bf16, bool lean, hipStream_t stream);
+                       bool out_bf16, hipStream_t stream);
 
 // Silero VAD model inputs (sfe_vad.hip): [64 context | 512 window] f32 per
 // 512-sample window (src/long_form/vad.rs:62-99, src/constants.rs).

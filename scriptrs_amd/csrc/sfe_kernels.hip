@@ -891,16 +891,6 @@ __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const flo
   norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, xcd_pair_work(blockIdx.x), pad_to, out);
 }
 
-// Lean variant: 4 waves over 32-feature slabs, no register holding (three
-// passes), at most 96 VGPRs and about 20 KB LDS so a workgroup fits beside
-// two log-mel workgroups on a CU.
-template <typename O>
-__global__ __launch_bounds__(64 * 4, 5) void sfe_norm_stream_kernel(const float* __restrict__ raw,
-                                                                    const Item* __restrict__ items, int n_items,
-                                                                    int pad_to, O* __restrict__ out) {
-  norm_body<4, 32, 0>(raw, items, n_items, blockIdx.x, pad_to, out);
-}
-
 }  // namespace
 
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
@@ -925,13 +915,8 @@ hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const It
 }
 
 template <typename O>
-hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, int pad_to, O* out, bool lean,
+hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, int pad_to, O* out,
                          hipStream_t stream) {
-  if (lean) {
-    const unsigned blocks = (unsigned)((int64_t)n_items * NormShape<4, 32>::kSlabs);
-    sfe_norm_stream_kernel<O><<<dim3(blocks), dim3(64 * 4), 0, stream>>>(raw, items, n_items, pad_to, out);
-    return hipGetLastError();
-  }
   using S = NormShape<kNormMainWaves, kNormMainSlab>;
   // whole groups of 16 workgroups (xcd_pair_work); the extra ones exit
   const unsigned blocks = (unsigned)(((int64_t)n_items * S::kSlabs + 15) / 16 * 16);
@@ -946,10 +931,10 @@ hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int m
 }
 
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, int pad_to, void* out,
-                       bool out_bf16, bool lean, hipStream_t stream) {
+                       bool out_bf16, hipStream_t stream) {
   if (n_items <= 0) return hipSuccess;
-  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, pad_to, static_cast<uint16_t*>(out), lean, stream);
-  return launch_norm_t(raw, items, n_items, max_T, pad_to, static_cast<float*>(out), lean, stream);
+  if (out_bf16) return launch_norm_t(raw, items, n_items, max_T, pad_to, static_cast<uint16_t*>(out), stream);
+  return launch_norm_t(raw, items, n_items, max_T, pad_to, static_cast<float*>(out), stream);
 }
 
 }  // namespace sfe

@@ -158,13 +158,13 @@ def test_streamed_sparse_tasks_equal_resident(extractor, window):
     assert torch.equal(a, b)
 
 
-def test_long_form_batched_pipeline(extractor):
-    """A call large enough to run as several log-mel batches with the lean
-    normalisation overlapping on the aux stream: frame offsets exact for every
-    chunk, values checked on chunks around every batch boundary."""
+def test_long_form_large_call(extractor):
+    """A 36 M-sample long form in one call (175 chunk tasks, so every
+    log-mel workgroup spans item boundaries): frame offsets exact for every
+    chunk, values checked on chunks at the ends and around each quarter."""
     import torch
     from scriptrs_amd import build_fast_execution_plan
-    _flush("case: long form 36M samples (batched pipeline)")
+    _flush("case: long form 36M samples")
     rec = synth.speech_like(36_000_000, 21)
     tasks = build_fast_execution_plan(rec.size)
     assert sum(((t.audio_end - t.audio_start) // 160 + 1 + 15) // 16 for t in tasks) >= 4 * 4096
