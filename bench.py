@@ -40,20 +40,26 @@ sys.path.insert(0, ROOT)
 
 SR = 16_000
 HBM_PEAK_GBS = 8000.0
+VALU_PEAK_INSTS_PER_S = 256 * 4 * 2.4e9 / 4  # CUs x SIMDs x clock / 4 cycles per wave64 instruction
 
 
-def measured_traffic(fname: str, applies: bool):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE runs (each scaled by what the counter reads for a plain copy),
-    or None.  Only valid for the kernel source those runs measured, whose
-    sha256 the file records."""
+def measured_profile(fname: str, applies: bool, key: str = "traffic_bytes"):
+    """A per-launch figure from the committed rocprofv3 counter runs, or None:
+    traffic_bytes (FETCH_SIZE / WRITE_SIZE, each scaled by what the counter
+    reads for a plain copy) or valu_insts_per_launch (SQ_INSTS_VALU).  Only
+    valid for the kernel source those runs measured, whose sha256 the file
+    records."""
     import hashlib
     tfile = os.path.join(ROOT, "profiles", fname)
     if not applies or not os.path.exists(tfile):
         return None
     t = json.load(open(tfile))
     src = open(os.path.join(ROOT, t["kernel_source"]), "rb").read()
-    return t["traffic_bytes"] if hashlib.sha256(src).hexdigest() == t["kernel_source_sha256"] else None
+    return t.get(key) if hashlib.sha256(src).hexdigest() == t["kernel_source_sha256"] else None
+
+
+def measured_traffic(fname: str, applies: bool):
+    return measured_profile(fname, applies)
 
 
 def make_workload(name: str):
@@ -202,6 +208,16 @@ def main() -> int:
         "kernels_ms": {"sfe_logmel_kernel": logmel_ms, "sfe_norm_kernel": norm_ms},
         "path_gbps": alg_path / sec / 1e9,
     }
+    # The log-mel kernel is bound by VALU issue, not HBM: its instruction
+    # count (SQ_INSTS_VALU) against MI355X's vector issue peak, one wave64
+    # fp32 instruction per SIMD per 4 cycles at 2.4 GHz (157.3 TFLOP/s counts
+    # packed FMA: 4 flops per lane-instruction).
+    valu = measured_profile("sfe_logmel_longform_1h_traffic.json",
+                            args.workload == "config3" and args.pcm == "f32", "valu_insts_per_launch")
+    if valu:
+        peak = VALU_PEAK_INSTS_PER_S
+        result["valu_bound"] = {"insts_per_launch": valu, "peak_insts_per_s": peak,
+                                "floor_ms": valu / peak * 1e3, "frac": valu / peak * 1e3 / logmel_ms}
     if streamed:
         result["h2d_gbps"] = in_bytes * n_audio / sec / 1e9
         result["config"]["window_samples"] = args.window_samples
