@@ -3,6 +3,8 @@ import sys
 
 import pytest
 
+from parity import ATOL, RTOL, assert_close, assert_parity  # noqa: F401
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
@@ -10,57 +12,6 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
-
-
-# Parity bar for normalised log-mel (north_star): 1e-4 absolute + 1e-3 relative.
-ATOL = 1e-4
-RTOL = 1e-3
-
-
-def assert_close(got, want, atol=ATOL, rtol=RTOL, what=""):
-    import numpy as np
-    got = np.asarray(got, np.float64)
-    want = np.asarray(want, np.float64)
-    assert got.shape == want.shape, (got.shape, want.shape)
-    nan_g, nan_w = np.isnan(got), np.isnan(want)
-    assert np.array_equal(nan_g, nan_w), f"{what}: NaN pattern differs"
-    g, w = got[~nan_g], want[~nan_w]
-    err = np.abs(g - w)
-    bad = err > atol + rtol * np.abs(w)
-    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside tol, max abs err {err.max():.3e}"
-    return float(err.max()) if err.size else 0.0
-
-
-def assert_parity(got, oracle_out, ref64, env, atol=ATOL, rtol=RTOL, what=""):
-    """GPU vs oracle at the north-star bar, widened only by the f32 noise envelope.
-
-    The oracle and the reference both compute in f32.  Where a mel bin's
-    energy sits near the 2^-24 guard, f32 FFT rounding moves the normalised
-    value by up to ~1e-3, so no two f32 implementations agree to 1e-4 there.
-    ``env`` (tests/np_reference.py:f32_noise_envelope) is the analytic scale
-    of that noise per element.  Checks, per element:
-      |got - ref64| <= atol + rtol*|ref64| + env         (GPU within f32 noise of exact)
-    and either
-      |got - oracle| <= atol + rtol*|oracle| + 2*env     (two f32 implementations agree)
-    or |got - ref64| <= |oracle - ref64|                 (GPU closer to exact than the
-                                                          oracle's radix-2 f32 FFT)
-    Returns (max |got-oracle|, number of elements that needed the widening)."""
-    import numpy as np
-    g = np.asarray(got, np.float64)
-    o = np.asarray(oracle_out, np.float64)
-    r = np.asarray(ref64, np.float64)
-    n = np.asarray(env, np.float64)
-    assert g.shape == o.shape == r.shape == n.shape, (g.shape, o.shape, r.shape, n.shape)
-    nan = np.isnan(o)
-    assert np.array_equal(np.isnan(g), nan), f"{what}: NaN pattern differs"
-    g, o, r, n = g[~nan], o[~nan], r[~nan], n[~nan]
-    base = atol + rtol * np.abs(o)
-    b1 = (np.abs(g - o) > base + 2 * n) & (np.abs(g - r) > np.abs(o - r))
-    b2 = np.abs(g - r) > atol + rtol * np.abs(r) + n
-    assert not b1.any(), f"{what}: {b1.sum()} of {b1.size} outside oracle bound, max {np.abs(g - o).max():.3e}"
-    assert not b2.any(), f"{what}: {b2.sum()} of {b2.size} outside f64 bound, max {np.abs(g - r).max():.3e}"
-    widened = int((np.abs(g - o) > base).sum())
-    return float(np.abs(g - o).max()) if g.size else 0.0, widened
 
 
 @pytest.fixture(scope="session")
