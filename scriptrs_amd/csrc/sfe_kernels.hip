@@ -555,7 +555,7 @@ constexpr int kNormFlush = 8;                  // f32 partial sums span at most 
 // Shape of a normalisation workgroup: W waves, a slab of F features.
 template <int W, int F>
 struct NormShape {
-  static_assert(F == 16 || F == 32, "slab of 16 or 32 features");
+  static_assert(F == 16, "slabs of 16 features (half a 128-byte frame line)");
   static constexpr int kThreads = 64 * W;
   static constexpr int kLanesPerFrame = F / 4;            // float4 per lane
   static constexpr int kGroup = 64 / kLanesPerFrame;      // frames per load instruction
@@ -714,8 +714,10 @@ __device__ __forceinline__ void stage(float* tb, int q, int col, const float4& v
   tb[(4 * q + 3) * ts + col] = v.w;
 }
 
-// W waves, slab of F features, N float4 registers per lane (N == 0: always
-// stream, the lean variant).  `work` is the (item, slab) index.
+// W waves, slab of F features, N float4 registers per lane: items of up to
+// kSpan * N frames are held in registers and read once; longer items take
+// the streaming path (three passes, the later ones mostly cache hits).
+// `work` is the (item, slab) index.
 template <int W, int F, int N, typename O>
 __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const Item* __restrict__ items,
                                           int n_items, int work, int pad_to, O* __restrict__ out) {
