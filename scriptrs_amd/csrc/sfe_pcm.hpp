@@ -32,12 +32,15 @@ __device__ __forceinline__ float pcm_div(float v, const Decode& d) {
 
 template <typename S>
 struct Pcm;
+// V4: 4 raw samples.  Recordings and item starts are only sample-aligned
+// (ragged batches start items anywhere), so the vector types carry the
+// sample's own alignment; gfx950 takes such addresses in one vector load.
 template <>
 struct Pcm<float> {
-  using V4 = float4;  // 4 raw samples
-  static __device__ __forceinline__ V4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  typedef float V4 __attribute__((ext_vector_type(4), aligned(4)));
+  static __device__ __forceinline__ V4 load4(const float* p) { return *reinterpret_cast<const V4*>(p); }
   static __device__ __forceinline__ float dec(float v, const Decode&) { return v; }
-  static __device__ __forceinline__ float4 dec4(const V4& v, const Decode&) { return v; }
+  static __device__ __forceinline__ float4 dec4(const V4& v, const Decode&) { return make_float4(v.x, v.y, v.z, v.w); }
 };
 template <>
 struct Pcm<int16_t> {

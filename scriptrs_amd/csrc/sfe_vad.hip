@@ -34,20 +34,6 @@ constexpr int kVadVecPerThread = kVadRowsPerBlock * kVadRowVec / kVadThreads;  /
 static_assert(kVadRowsPerBlock * kVadRowVec % kVadThreads == 0, "whole float4s per thread");
 static_assert(kVadCtx % 4 == 0 && kVadWin % 4 == 0, "rows start on float4 boundaries of the recording");
 
-// Four consecutive samples starting at a multiple of 4; f32 recordings only
-// need 4-byte alignment (global loads take unaligned dwordx4 addresses).
-template <typename S>
-struct VadLoad {
-  static __device__ __forceinline__ float4 get(const S* p, const Decode& d) { return Pcm<S>::dec4(Pcm<S>::load4(p), d); }
-};
-template <>
-struct VadLoad<float> {
-  typedef float V4 __attribute__((ext_vector_type(4), aligned(4)));
-  static __device__ __forceinline__ float4 get(const float* p, const Decode&) {
-    const V4 v = *reinterpret_cast<const V4*>(p);
-    return make_float4(v.x, v.y, v.z, v.w);
-  }
-};
 
 template <typename S>
 __device__ __forceinline__ float vad_sample(const S* x, int64_t len, int64_t i, const Decode& d) {
@@ -75,7 +61,7 @@ __global__ __launch_bounds__(kVadThreads) void sfe_vad_frames_kernel(const S* __
     const int64_t i = w * kVadWin - kVadCtx + p;
     dst[k] = w < n_windows ? w * kVadRow + p : -1;
     if (i >= 0 && i + 4 <= len) {
-      v[k] = VadLoad<S>::get(x + i, dc);
+      v[k] = Pcm<S>::dec4(Pcm<S>::load4(x + i), dc);
     } else {
       v[k] = make_float4(vad_sample(x, len, i, dc), vad_sample(x, len, i + 1, dc), vad_sample(x, len, i + 2, dc),
                          vad_sample(x, len, i + 3, dc));

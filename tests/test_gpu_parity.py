@@ -209,6 +209,50 @@ def test_encoder_input_layout(extractor):
         assert not enc[i, :, T:].any(), i
 
 
+def test_encoder_input_layout_bf16(extractor):
+    """The encoder layout in bf16: the packed bf16 output in the first T
+    columns, zeros after."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: encoder input layout bf16")
+    rec = synth.speech_like(700_000, 27)
+    tasks = build_fast_execution_plan(rec.size)
+    dev = torch.from_numpy(rec).cuda()
+    packed, fo = extractor.extract_chunks(dev, tasks, dtype="bf16")
+    enc, ff = extractor.extract_chunks_encoder_input(dev, tasks, dtype="bf16")
+    torch.cuda.synchronize()
+    assert enc.dtype == torch.bfloat16 and tuple(enc.shape) == (len(tasks), 128, 1501)
+    for i in range(len(tasks)):
+        T = int(ff[i])
+        want = packed[128 * fo[i]:128 * fo[i + 1]].reshape(128, T)
+        assert torch.equal(enc[i, :, :T], want), i
+        assert not enc[i, :, T:].any(), i
+
+
+def test_recording_at_4_byte_offset(extractor):
+    """A device recording that starts 4 bytes past a 16-byte boundary (a
+    slice of a larger buffer): bit-identical to the same samples at an
+    aligned address, for the chunk path and a ragged batch."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: recording at a 4-byte offset")
+    rec = synth.speech_like(900_001, 33)
+    tasks = build_fast_execution_plan(rec.size - 1)
+    big = torch.from_numpy(rec).cuda()
+    off = big[1:]
+    assert off.data_ptr() % 16 == 4
+    aligned = off.clone()
+    assert aligned.data_ptr() % 16 == 0
+    a, fa = extractor.extract_chunks(aligned, tasks)
+    b, fb = extractor.extract_chunks(off, tasks)
+    offsets = np.array([0, 160_001, 400_003, 900_000], np.int64)
+    c, fc = extractor.extract_batch(aligned, offsets)
+    d, fd = extractor.extract_batch(off, offsets)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb) and torch.equal(a, b)
+    assert np.array_equal(fc, fd) and torch.equal(c, d)
+
+
 def test_encoder_input_rejects_overlong_chunk(extractor):
     import torch
     from scriptrs_amd import ChunkTask
