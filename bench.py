@@ -47,15 +47,18 @@ def measured_profile(fname: str, applies: bool, key: str = "traffic_bytes"):
     """A per-launch figure from the committed rocprofv3 counter runs, or None:
     traffic_bytes (FETCH_SIZE / WRITE_SIZE, each scaled by what the counter
     reads for a plain copy) or valu_insts_per_launch (SQ_INSTS_VALU).  Only
-    valid for the kernel source those runs measured, whose sha256 the file
-    records."""
+    valid for the kernel sources those runs measured: the file records the
+    sha256 of their concatenation."""
     import hashlib
     tfile = os.path.join(ROOT, "profiles", fname)
     if not applies or not os.path.exists(tfile):
         return None
     t = json.load(open(tfile))
-    src = open(os.path.join(ROOT, t["kernel_source"]), "rb").read()
-    return t.get(key) if hashlib.sha256(src).hexdigest() == t["kernel_source_sha256"] else None
+    files = t["kernel_source"]
+    h = hashlib.sha256()
+    for f in [files] if isinstance(files, str) else files:
+        h.update(open(os.path.join(ROOT, f), "rb").read())
+    return t.get(key) if h.hexdigest() == t["kernel_source_sha256"] else None
 
 
 def measured_traffic(fname: str, applies: bool):
