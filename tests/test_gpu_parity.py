@@ -433,3 +433,49 @@ def test_config3_full_invariants(extractor):
         a = rec[s:e]
         got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
         assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
+
+
+@pytest.mark.parametrize("seed", [101, 202, 303])
+def test_random_ragged_batch(extractor, seed):
+    """48 clips of random lengths from 1 sample to 25 s (a few tiny ones
+    forced), each checked against the oracle."""
+    import torch
+    _flush(f"case: random ragged batch seed {seed}")
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, 400_000, 48)
+    lens[:4] = [1, 2, 159, 161]
+    rng.shuffle(lens)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    flat = synth.sinusoids(int(off[-1]), seed)
+    out, fo = extractor.extract_batch(torch.from_numpy(flat).cuda(), off)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    assert np.array_equal(fo, np.concatenate([[0], np.cumsum(lens // 160 + 1)]))
+    for i in range(len(lens)):
+        a = flat[off[i]:off[i + 1]]
+        got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"clip {i} len {lens[i]}")
+
+
+@pytest.mark.parametrize("seed", [404, 505])
+def test_random_chunk_tables(extractor, seed):
+    """Chunk tasks at random, unsorted and overlapping positions of one
+    recording (the resident path takes any order), each checked against the
+    oracle on its own span."""
+    import torch
+    from scriptrs_amd import ChunkTask
+    _flush(f"case: random chunk table seed {seed}")
+    rng = np.random.default_rng(seed)
+    rec = synth.speech_like(3_000_000, seed)
+    tasks = []
+    for _ in range(40):
+        n = int(rng.integers(1, 240_001))
+        s = int(rng.integers(0, rec.size - n + 1))
+        tasks.append(ChunkTask(s, s + n, s, 0))
+    out, fo = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for i, t in enumerate(tasks):
+        a = rec[t.audio_start:t.audio_end]
+        got = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"task {i}")
