@@ -9,7 +9,9 @@
 #include <string.h>
 
 #include <algorithm>
+#include <exception>
 #include <mutex>
+#include <new>
 #include <string>
 #include <thread>
 #include <vector>
@@ -294,6 +296,27 @@ int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, i
   return SFE_OK;
 }
 
+// Runs an entry point's body and turns a C++ exception (host allocation
+// failure, thread creation failure) into a status: no exception crosses the
+// C ABI.
+template <class F>
+int guarded(F&& body) {
+  try {
+    return body();
+  } catch (const std::bad_alloc&) {
+    g_last_error.clear();  // assigning a message could throw again
+    return SFE_HIP_ERROR;
+  } catch (const std::exception& e) {
+    try {
+      return fail(SFE_HIP_ERROR, std::string("host error: ") + e.what());
+    } catch (...) {
+      return SFE_HIP_ERROR;
+    }
+  } catch (...) {
+    return SFE_HIP_ERROR;
+  }
+}
+
 Source f32_source(const float* p) { return Source{p, sfe::kPcmF32, 1.0f, sizeof(float)}; }
 
 // The reference's WAV decode divisor: ((1 << (bits - 1)) - 1) as f32
@@ -357,87 +380,93 @@ int64_t sfe_max_feature_frames(const sfe_config* cfg) {
 
 int sfe_plan_fast(const sfe_overlap_config* cfg, int64_t audio_len, sfe_chunk* tasks, int32_t cap,
                   int32_t* n_out) {
-  if (!cfg || !n_out) return fail(SFE_INVALID_ARG, "null argument");
-  if (audio_len < 0) return fail(SFE_INVALID_ARG, "negative audio length");
-  const int64_t spf = 1280;  // SAMPLES_PER_ENCODER_FRAME, src/constants.rs:4-5
-  const int64_t hop = 160;   // MEL_HOP_SAMPLES
-  auto sat = [](int64_t a, int64_t b) { return a > b ? a - b : (int64_t)0; };
-  // chunk_samples / overlap_samples / stride_samples: src/long_form/planner.rs:105-122
-  int64_t raw = std::max(sat(sat(cfg->max_model_samples, cfg->context_samples), hop), spf);
-  const int64_t chunk = raw / spf * spf;
-  double req_d = cfg->overlap_seconds * 16000.0;
-  int64_t req = req_d != req_d || req_d <= 0.0 ? 0 : (req_d >= 9.2e18 ? INT64_MAX : (int64_t)req_d);
-  const int64_t overlap = std::min(req, chunk / 2) / spf * spf;
-  const int64_t stride = std::max(sat(chunk, overlap), spf) / spf * spf;
-  // plan (planner.rs:124-137) + push_overlap_task (long_form.rs:566-582)
-  int64_t count = 0;
-  int64_t start = 0;
-  while (start < audio_len) {
-    int64_t end = std::min(start + chunk, audio_len);
-    if (tasks && count < cap) {
-      int64_t ctx_start = sat(start, cfg->context_samples);
-      tasks[count] = {ctx_start, end, start, start - ctx_start};
+  return guarded([&]() -> int {
+    if (!cfg || !n_out) return fail(SFE_INVALID_ARG, "null argument");
+    if (audio_len < 0) return fail(SFE_INVALID_ARG, "negative audio length");
+    const int64_t spf = 1280;  // SAMPLES_PER_ENCODER_FRAME, src/constants.rs:4-5
+    const int64_t hop = 160;   // MEL_HOP_SAMPLES
+    auto sat = [](int64_t a, int64_t b) { return a > b ? a - b : (int64_t)0; };
+    // chunk_samples / overlap_samples / stride_samples: src/long_form/planner.rs:105-122
+    int64_t raw = std::max(sat(sat(cfg->max_model_samples, cfg->context_samples), hop), spf);
+    const int64_t chunk = raw / spf * spf;
+    double req_d = cfg->overlap_seconds * 16000.0;
+    int64_t req = req_d != req_d || req_d <= 0.0 ? 0 : (req_d >= 9.2e18 ? INT64_MAX : (int64_t)req_d);
+    const int64_t overlap = std::min(req, chunk / 2) / spf * spf;
+    const int64_t stride = std::max(sat(chunk, overlap), spf) / spf * spf;
+    // plan (planner.rs:124-137) + push_overlap_task (long_form.rs:566-582)
+    int64_t count = 0;
+    int64_t start = 0;
+    while (start < audio_len) {
+      int64_t end = std::min(start + chunk, audio_len);
+      if (tasks && count < cap) {
+        int64_t ctx_start = sat(start, cfg->context_samples);
+        tasks[count] = {ctx_start, end, start, start - ctx_start};
+      }
+      ++count;
+      if (end == audio_len) break;
+      start += stride;
     }
-    ++count;
-    if (end == audio_len) break;
-    start += stride;
-  }
-  if (count > INT32_MAX) return fail(SFE_INVALID_ARG, "too many tasks");
-  *n_out = (int32_t)count;
-  if (count > cap || (!tasks && count > 0)) return fail(SFE_INVALID_ARG, "task buffer too small");
-  return SFE_OK;
+    if (count > INT32_MAX) return fail(SFE_INVALID_ARG, "too many tasks");
+    *n_out = (int32_t)count;
+    if (count > cap || (!tasks && count > 0)) return fail(SFE_INVALID_ARG, "task buffer too small");
+    return SFE_OK;
+  });
 }
 
 int sfe_build_tables(const sfe_config* cfg, float* window, float* filterbank) {
-  if (!cfg || cfg->win_length <= 1 || cfg->n_fft <= 0 || cfg->feature_size <= 0 || cfg->sample_rate <= 0)
-    return fail(SFE_INVALID_ARG, "invalid config");
-  if (window) sfe::hann_window(cfg->win_length, window);
-  if (filterbank) sfe::mel_filterbank(cfg->n_fft, cfg->feature_size, cfg->sample_rate, filterbank);
-  return SFE_OK;
+  return guarded([&]() -> int {
+    if (!cfg || cfg->win_length <= 1 || cfg->n_fft <= 0 || cfg->feature_size <= 0 || cfg->sample_rate <= 0)
+      return fail(SFE_INVALID_ARG, "invalid config");
+    if (window) sfe::hann_window(cfg->win_length, window);
+    if (filterbank) sfe::mel_filterbank(cfg->n_fft, cfg->feature_size, cfg->sample_rate, filterbank);
+    return SFE_OK;
+  });
 }
 
 const char* sfe_last_error(void) { return g_last_error.c_str(); }
 
 int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
-  if (!cfg || !out) return fail(SFE_INVALID_ARG, "null argument");
-  *out = nullptr;
-  std::string why;
-  if (!shape_supported(cfg, &why)) return fail(SFE_INVALID_ARG, why);
-  sfe::DevTables host;
-  if (!sfe::build_dev_tables(cfg->sample_rate, &host))
-    return fail(SFE_INVALID_ARG, "mel filter wider than the kernel's band table");
-  int ndev = 0;
-  hipError_t e = hipGetDeviceCount(&ndev);
-  if (e != hipSuccess || ndev == 0) return fail(SFE_HIP_ERROR, "no HIP device available");
-  if (device < 0 || device >= ndev) return fail(SFE_INVALID_ARG, "device index out of range");
-  SFE_HIP(hipSetDevice(device));
-  sfe_ctx* ctx = new sfe_ctx();
-  ctx->cfg = *cfg;
-  ctx->device = device;
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
-    ctx->grid_cap = cus * sfe::kLogmelBlocksPerCU;
-  auto cleanup = [&](int rc) {
-    sfe_destroy(ctx);
-    return rc;
-  };
-  if ((e = hipMalloc(&ctx->d_tables, sizeof(sfe::DevTables))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc"));
-  if ((e = hipMemcpy(ctx->d_tables, &host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
-    return cleanup(hip_fail(e, "hipMemcpy"));
-  if ((e = hipStreamCreateWithFlags(&ctx->s_compute, hipStreamNonBlocking)) != hipSuccess)
-    return cleanup(hip_fail(e, "hipStreamCreate"));
-  if ((e = hipStreamCreateWithFlags(&ctx->s_copy, hipStreamNonBlocking)) != hipSuccess)
-    return cleanup(hip_fail(e, "hipStreamCreate"));
-  if ((e = hipEventCreateWithFlags(&ctx->ev_last, hipEventDisableTiming)) != hipSuccess)
-    return cleanup(hip_fail(e, "hipEventCreate"));
-  for (int i = 0; i < 2; ++i) {
-    if ((e = hipEventCreateWithFlags(&ctx->ev_copied[i], hipEventDisableTiming)) != hipSuccess)
+  return guarded([&]() -> int {
+    if (!cfg || !out) return fail(SFE_INVALID_ARG, "null argument");
+    *out = nullptr;
+    std::string why;
+    if (!shape_supported(cfg, &why)) return fail(SFE_INVALID_ARG, why);
+    sfe::DevTables host;
+    if (!sfe::build_dev_tables(cfg->sample_rate, &host))
+      return fail(SFE_INVALID_ARG, "mel filter wider than the kernel's band table");
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0) return fail(SFE_HIP_ERROR, "no HIP device available");
+    if (device < 0 || device >= ndev) return fail(SFE_INVALID_ARG, "device index out of range");
+    SFE_HIP(hipSetDevice(device));
+    sfe_ctx* ctx = new sfe_ctx();
+    ctx->cfg = *cfg;
+    ctx->device = device;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+      ctx->grid_cap = cus * sfe::kLogmelBlocksPerCU;
+    auto cleanup = [&](int rc) {
+      sfe_destroy(ctx);
+      return rc;
+    };
+    if ((e = hipMalloc(&ctx->d_tables, sizeof(sfe::DevTables))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc"));
+    if ((e = hipMemcpy(ctx->d_tables, &host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
+      return cleanup(hip_fail(e, "hipMemcpy"));
+    if ((e = hipStreamCreateWithFlags(&ctx->s_compute, hipStreamNonBlocking)) != hipSuccess)
+      return cleanup(hip_fail(e, "hipStreamCreate"));
+    if ((e = hipStreamCreateWithFlags(&ctx->s_copy, hipStreamNonBlocking)) != hipSuccess)
+      return cleanup(hip_fail(e, "hipStreamCreate"));
+    if ((e = hipEventCreateWithFlags(&ctx->ev_last, hipEventDisableTiming)) != hipSuccess)
       return cleanup(hip_fail(e, "hipEventCreate"));
-    if ((e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming)) != hipSuccess)
-      return cleanup(hip_fail(e, "hipEventCreate"));
-  }
-  *out = ctx;
-  return SFE_OK;
+    for (int i = 0; i < 2; ++i) {
+      if ((e = hipEventCreateWithFlags(&ctx->ev_copied[i], hipEventDisableTiming)) != hipSuccess)
+        return cleanup(hip_fail(e, "hipEventCreate"));
+      if ((e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming)) != hipSuccess)
+        return cleanup(hip_fail(e, "hipEventCreate"));
+    }
+    *out = ctx;
+    return SFE_OK;
+  });
 }
 
 void sfe_destroy(sfe_ctx* ctx) {
@@ -464,62 +493,68 @@ void sfe_destroy(sfe_ctx* ctx) {
 }
 
 int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64_t out_capacity) {
-  if (len <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty");
-  if (!audio || !out) return fail(SFE_INVALID_ARG, "null buffer");
-  int rc = check_ctx(ctx);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  const int64_t T = len / sfe::kHop + 1;
-  const int64_t nout = T * sfe::kMel;
-  if (out_capacity < nout) return fail(SFE_INVALID_ARG, "output buffer too small");
-  SFE_HIP(ctx->io_in.reserve((size_t)len * sizeof(float)));
-  SFE_HIP(ctx->io_out.reserve((size_t)nout * sizeof(float)));
-  hipStream_t s = ctx->s_compute;
-  SFE_HIP(hipMemcpyAsync(ctx->io_in.ptr, audio, (size_t)len * sizeof(float), hipMemcpyHostToDevice, s));
-  std::vector<Item> items;
-  int64_t start = 0, tiles = 0, fo[2];
-  if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
-  if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
-    return rc;
-  SFE_HIP(hipMemcpyAsync(out, ctx->io_out.ptr, (size_t)nout * sizeof(float), hipMemcpyDeviceToHost, s));
-  SFE_HIP(hipStreamSynchronize(s));
-  return SFE_OK;
+  return guarded([&]() -> int {
+    if (len <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty");
+    if (!audio || !out) return fail(SFE_INVALID_ARG, "null buffer");
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    const int64_t T = len / sfe::kHop + 1;
+    const int64_t nout = T * sfe::kMel;
+    if (out_capacity < nout) return fail(SFE_INVALID_ARG, "output buffer too small");
+    SFE_HIP(ctx->io_in.reserve((size_t)len * sizeof(float)));
+    SFE_HIP(ctx->io_out.reserve((size_t)nout * sizeof(float)));
+    hipStream_t s = ctx->s_compute;
+    SFE_HIP(hipMemcpyAsync(ctx->io_in.ptr, audio, (size_t)len * sizeof(float), hipMemcpyHostToDevice, s));
+    std::vector<Item> items;
+    int64_t start = 0, tiles = 0, fo[2];
+    if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
+    if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
+      return rc;
+    SFE_HIP(hipMemcpyAsync(out, ctx->io_out.ptr, (size_t)nout * sizeof(float), hipMemcpyDeviceToHost, s));
+    SFE_HIP(hipStreamSynchronize(s));
+    return SFE_OK;
+  });
 }
 
 int sfe_prepare_chunk(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64_t out_capacity,
                       int64_t* feature_frames) {
-  if (len <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty");
-  if (!ctx) return fail(SFE_INVALID_ARG, "null context");
-  if (len > ctx->cfg.max_audio_samples) {
-    char buf[160];
-    snprintf(buf, sizeof buf, "audio exceeds the single-chunk limit: actual=%.2fs max=%.2fs",
-             (double)len / ctx->cfg.sample_rate, (double)ctx->cfg.max_audio_samples / ctx->cfg.sample_rate);
-    return fail(SFE_AUDIO_TOO_LONG, buf);
-  }
-  int rc = sfe_extract(ctx, audio, len, out, out_capacity);
-  if (rc == SFE_OK && feature_frames) *feature_frames = len / sfe::kHop + 1;
-  return rc;
+  return guarded([&]() -> int {
+    if (len <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty");
+    if (!ctx) return fail(SFE_INVALID_ARG, "null context");
+    if (len > ctx->cfg.max_audio_samples) {
+      char buf[160];
+      snprintf(buf, sizeof buf, "audio exceeds the single-chunk limit: actual=%.2fs max=%.2fs",
+               (double)len / ctx->cfg.sample_rate, (double)ctx->cfg.max_audio_samples / ctx->cfg.sample_rate);
+      return fail(SFE_AUDIO_TOO_LONG, buf);
+    }
+    int rc = sfe_extract(ctx, audio, len, out, out_capacity);
+    if (rc == SFE_OK && feature_frames) *feature_frames = len / sfe::kHop + 1;
+    return rc;
+  });
 }
 
 int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets, int32_t n, int32_t out_dtype,
                       void* out, int64_t* frame_offsets, void* stream) {
-  if (n <= 0 || !offsets || !samples || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid batch arguments");
-  int rc = check_dtype(out_dtype);
-  if (rc) return rc;
-  std::vector<int64_t> starts(n), lens(n);
-  for (int32_t i = 0; i < n; ++i) {
-    if (offsets[i + 1] < offsets[i] || offsets[i] < 0)
-      return fail(SFE_INVALID_ARG, "offsets must be non-negative and non-decreasing");
-    starts[i] = offsets[i];
-    lens[i] = offsets[i + 1] - offsets[i];
-  }
-  if ((rc = check_ctx(ctx))) return rc;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  std::vector<Item> items;
-  int64_t tiles = 0;
-  if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-  return run_items(ctx, f32_source(samples), items, tiles, frame_offsets[n], out_dtype, out,
-                   static_cast<hipStream_t>(stream));
+  return guarded([&]() -> int {
+    if (n <= 0 || !offsets || !samples || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid batch arguments");
+    int rc = check_dtype(out_dtype);
+    if (rc) return rc;
+    std::vector<int64_t> starts(n), lens(n);
+    for (int32_t i = 0; i < n; ++i) {
+      if (offsets[i + 1] < offsets[i] || offsets[i] < 0)
+        return fail(SFE_INVALID_ARG, "offsets must be non-negative and non-decreasing");
+      starts[i] = offsets[i];
+      lens[i] = offsets[i + 1] - offsets[i];
+    }
+    if ((rc = check_ctx(ctx))) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    std::vector<Item> items;
+    int64_t tiles = 0;
+    if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
+    return run_items(ctx, f32_source(samples), items, tiles, frame_offsets[n], out_dtype, out,
+                     static_cast<hipStream_t>(stream));
+  });
 }
 
 int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
@@ -530,85 +565,91 @@ int sfe_extract_chunks(sfe_ctx* ctx, const float* recording, int64_t len, const 
 int sfe_extract_chunks_pcm(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample,
                            int64_t len, const sfe_chunk* tasks, int32_t n, int32_t out_dtype, void* out,
                            int64_t* frame_offsets, void* stream) {
-  if (n <= 0 || !tasks || !recording || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
-  int rc = check_dtype(out_dtype);
-  if (rc) return rc;
-  Source src;
-  if ((rc = pcm_source(recording, pcm_format, bits_per_sample, &src))) return rc;
-  std::vector<int64_t> starts(n), lens(n);
-  for (int32_t i = 0; i < n; ++i) {
-    const sfe_chunk& t = tasks[i];
-    if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
-      return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
-    starts[i] = t.audio_start;
-    lens[i] = t.audio_end - t.audio_start;
-  }
-  if ((rc = check_ctx(ctx))) return rc;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  std::vector<Item> items;
-  int64_t tiles = 0;
-  if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-  return run_items(ctx, src, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+  return guarded([&]() -> int {
+    if (n <= 0 || !tasks || !recording || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+    int rc = check_dtype(out_dtype);
+    if (rc) return rc;
+    Source src;
+    if ((rc = pcm_source(recording, pcm_format, bits_per_sample, &src))) return rc;
+    std::vector<int64_t> starts(n), lens(n);
+    for (int32_t i = 0; i < n; ++i) {
+      const sfe_chunk& t = tasks[i];
+      if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+        return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+      starts[i] = t.audio_start;
+      lens[i] = t.audio_end - t.audio_start;
+    }
+    if ((rc = check_ctx(ctx))) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    std::vector<Item> items;
+    int64_t tiles = 0;
+    if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
+    return run_items(ctx, src, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+  });
 }
 
 int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
                               int32_t target_frames, int32_t out_dtype, void* out, int64_t* feature_frames,
                               void* stream) {
-  if (n <= 0 || !tasks || !recording || !out || !feature_frames || target_frames <= 0)
-    return fail(SFE_INVALID_ARG, "invalid chunk arguments");
-  int rc = check_dtype(out_dtype);
-  if (rc) return rc;
-  std::vector<int64_t> starts(n), lens(n), fo(n + 1);
-  for (int32_t i = 0; i < n; ++i) {
-    const sfe_chunk& t = tasks[i];
-    if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
-      return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
-    starts[i] = t.audio_start;
-    lens[i] = t.audio_end - t.audio_start;
-  }
-  if ((rc = check_ctx(ctx))) return rc;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  std::vector<Item> items;
-  int64_t tiles = 0;
-  if ((rc = build_items(starts.data(), lens.data(), n, &items, fo.data(), &tiles))) return rc;
-  for (int32_t i = 0; i < n; ++i) {
-    // EncoderInputBuffer::copy_from_features rejects more frames than the
-    // encoder input holds (src/model.rs:259-264)
-    if (items[i].T > target_frames)
-      return fail(SFE_INVALID_ARG, "feature frame count " + std::to_string(items[i].T) + " exceeded encoder target " +
-                                       std::to_string(target_frames));
-    items[i].dst_off = (int64_t)i * sfe::kMel * target_frames;
-    feature_frames[i] = items[i].T;
-  }
-  return run_items(ctx, f32_source(recording), items, tiles, fo[n], out_dtype, out, static_cast<hipStream_t>(stream),
-                   target_frames);
+  return guarded([&]() -> int {
+    if (n <= 0 || !tasks || !recording || !out || !feature_frames || target_frames <= 0)
+      return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+    int rc = check_dtype(out_dtype);
+    if (rc) return rc;
+    std::vector<int64_t> starts(n), lens(n), fo(n + 1);
+    for (int32_t i = 0; i < n; ++i) {
+      const sfe_chunk& t = tasks[i];
+      if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+        return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+      starts[i] = t.audio_start;
+      lens[i] = t.audio_end - t.audio_start;
+    }
+    if ((rc = check_ctx(ctx))) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    std::vector<Item> items;
+    int64_t tiles = 0;
+    if ((rc = build_items(starts.data(), lens.data(), n, &items, fo.data(), &tiles))) return rc;
+    for (int32_t i = 0; i < n; ++i) {
+      // EncoderInputBuffer::copy_from_features rejects more frames than the
+      // encoder input holds (src/model.rs:259-264)
+      if (items[i].T > target_frames)
+        return fail(SFE_INVALID_ARG, "feature frame count " + std::to_string(items[i].T) + " exceeded encoder target " +
+                                         std::to_string(target_frames));
+      items[i].dst_off = (int64_t)i * sfe::kMel * target_frames;
+      feature_frames[i] = items[i].T;
+    }
+    return run_items(ctx, f32_source(recording), items, tiles, fo[n], out_dtype, out, static_cast<hipStream_t>(stream),
+                     target_frames);
+  });
 }
 
 int64_t sfe_vad_num_windows(int64_t len) { return sfe::vad_num_windows(len); }
 
 int sfe_vad_frames(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int32_t bits_per_sample, int64_t len,
                    float* out, int64_t out_windows, void* stream) {
-  if (len < 0) return fail(SFE_INVALID_ARG, "negative recording length");
-  Source src;
-  int rc = pcm_source(recording, pcm_format, bits_per_sample, &src);
-  if (rc) return rc;
-  const int64_t n = sfe::vad_num_windows(len);
-  if (n == 0) return SFE_OK;  // empty audio: no windows (src/long_form/vad.rs:67-69)
-  if (!recording || !out) return fail(SFE_INVALID_ARG, "null recording or output");
-  if (out_windows < n)
-    return fail(SFE_INVALID_ARG, "output holds " + std::to_string(out_windows) + " windows, " + std::to_string(n) +
-                                     " needed");
-  if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return fail(SFE_INVALID_ARG, "output must be 16-byte aligned");
-  if (reinterpret_cast<uintptr_t>(recording) % src.esize != 0)
-    return fail(SFE_INVALID_ARG, "recording is not aligned to its sample size");
-  if ((rc = check_ctx(ctx))) return rc;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(s, ctx->ev_last, 0));
-  SFE_HIP(sfe::launch_vad_frames(src.ptr, src.pcm, src.scale, len, out, s));
-  SFE_HIP(hipEventRecord(ctx->ev_last, s));
-  ctx->has_last = true;
-  return SFE_OK;
+  return guarded([&]() -> int {
+    if (len < 0) return fail(SFE_INVALID_ARG, "negative recording length");
+    Source src;
+    int rc = pcm_source(recording, pcm_format, bits_per_sample, &src);
+    if (rc) return rc;
+    const int64_t n = sfe::vad_num_windows(len);
+    if (n == 0) return SFE_OK;  // empty audio: no windows (src/long_form/vad.rs:67-69)
+    if (!recording || !out) return fail(SFE_INVALID_ARG, "null recording or output");
+    if (out_windows < n)
+      return fail(SFE_INVALID_ARG, "output holds " + std::to_string(out_windows) + " windows, " + std::to_string(n) +
+                                       " needed");
+    if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return fail(SFE_INVALID_ARG, "output must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(recording) % src.esize != 0)
+      return fail(SFE_INVALID_ARG, "recording is not aligned to its sample size");
+    if ((rc = check_ctx(ctx))) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(s, ctx->ev_last, 0));
+    SFE_HIP(sfe::launch_vad_frames(src.ptr, src.pcm, src.scale, len, out, s));
+    SFE_HIP(hipEventRecord(ctx->ev_last, s));
+    ctx->has_last = true;
+    return SFE_OK;
+  });
 }
 
 int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, const sfe_chunk* tasks, int32_t n,
@@ -620,167 +661,169 @@ int sfe_extract_chunks_streamed(sfe_ctx* ctx, const float* host, int64_t len, co
 int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, int32_t pcm_format,
                                     int32_t bits_per_sample, int64_t len, const sfe_chunk* tasks, int32_t n,
                                     int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples) {
-  const char* host = static_cast<const char*>(host_recording);
-  if (n <= 0 || !tasks || !host || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
-  int rc = check_dtype(out_dtype);
-  if (rc) return rc;
-  Source src;
-  if ((rc = pcm_source(host_recording, pcm_format, bits_per_sample, &src))) return rc;
-  const size_t es = src.esize;
-  std::vector<int64_t> starts(n), lens(n);
-  for (int32_t i = 0; i < n; ++i) {
-    const sfe_chunk& t = tasks[i];
-    if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
-      return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
-    if (t.audio_end - t.audio_start > window_samples)
-      return fail(SFE_INVALID_ARG, "window_samples is shorter than task " + std::to_string(i));
-    if (i > 0 && t.audio_start < tasks[i - 1].audio_start)
-      return fail(SFE_INVALID_ARG, "tasks must be ordered by audio_start");
-    starts[i] = t.audio_start;
-    lens[i] = t.audio_end - t.audio_start;
-  }
-  if ((rc = check_ctx(ctx))) return rc;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  std::vector<Item> items;
-  int64_t tiles = 0;
-  if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-
-  // Group tasks into windows [wstart, wend) no longer than window_samples;
-  // items are re-based to the window and their tiles to the group.
-  struct Group {
-    int32_t first, count;
-    int64_t wstart, wend;
-    int32_t tiles, max_T;
-  };
-  std::vector<Group> groups;
-  for (int32_t i = 0; i < n;) {
-    Group g{i, 0, items[i].start, items[i].start, 0, 0};
-    while (i < n && items[i].start + items[i].len - g.wstart <= window_samples) {
-      g.wend = std::max(g.wend, items[i].start + items[i].len);
-      ++i;
-      ++g.count;
-    }
-    groups.push_back(g);
-  }
-  // Batches of up to batch_windows consecutive windows.  A batch is copied
-  // as one recording range [start, end) into half (bi & 1) of the device
-  // buffer, so a window joins a batch only while that range stays within
-  // batch_windows * window_samples samples and the gaps between
-  // the batch's windows (copied but unused) add up to at most one window.
-  // Items are re-based to their half and their units numbered within the
-  // batch.
-  struct Batch {
-    size_t g0, g1;
-    int64_t start, end;
-  };
-  const size_t batch_windows =
-      std::min(kStreamMaxBatchWindows, std::max<size_t>(1, kStreamBatchBytes / ((size_t)window_samples * es)));
-  const int64_t half = (int64_t)batch_windows * window_samples;
-  std::vector<Batch> batches;
-  for (size_t gi = 0; gi < groups.size();) {
-    Batch bt{gi, gi + 1, groups[gi].wstart, groups[gi].wend};
-    int64_t covered = groups[gi].wend - groups[gi].wstart;
-    for (++gi; gi < groups.size() && bt.g1 - bt.g0 < batch_windows; ++gi) {
-      const int64_t end = std::max(bt.end, groups[gi].wend);
-      const int64_t cov = covered + (groups[gi].wend - groups[gi].wstart);
-      if (end - bt.start > half || (end - bt.start) - std::min(cov, end - bt.start) > window_samples) break;
-      bt.end = end;
-      covered = cov;
-      bt.g1 = gi + 1;
-    }
-    batches.push_back(bt);
-  }
-  for (size_t bi = 0; bi < batches.size(); ++bi) {
-    const int64_t base = (int64_t)(bi & 1) * half - batches[bi].start;
-    int32_t t = 0;
-    for (size_t gi = batches[bi].g0; gi < batches[bi].g1; ++gi) {
-      Group& g = groups[gi];
-      const int32_t t0 = t;
-      for (int32_t i = g.first; i < g.first + g.count; ++i) {
-        items[i].start += base;
-        items[i].tile_off = t;
-        t += (int32_t)sfe::tiles_for(items[i].T);
-        g.max_T = std::max(g.max_T, (int)items[i].T);
-      }
-      g.tiles = t - t0;
-    }
-  }
-  const size_t mbytes = items.size() * sizeof(Item);
-  ctx->meta_items.clear();  // the table uploaded below is re-based per window group
-  SFE_HIP(ctx->h_meta.reserve(mbytes));
-  SFE_HIP(ctx->meta.reserve(mbytes));
-  SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
-  float* raw = static_cast<float*>(ctx->scratch.ptr);
-  // A recording already in pinned (page-locked) host memory is copied to
-  // the device directly; pageable memory goes through two pinned staging
-  // windows.
-  bool pinned = false;
-  {
-    hipPointerAttribute_t attr;
-    if (hipPointerGetAttributes(&attr, host_recording) == hipSuccess) pinned = attr.type == hipMemoryTypeHost;
-    (void)hipGetLastError();  // a pageable pointer leaves an error code behind
-  }
-  SFE_HIP(ctx->win.reserve(2 * (size_t)half * es));
-  if (!pinned)
-    for (int b = 0; b < 2; ++b) SFE_HIP(ctx->h_win[b].reserve((size_t)half * es));
-  hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
-  if (ctx->has_last) {
-    SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_last, 0));
-    SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_last, 0));
-  }
-  memcpy(ctx->h_meta.ptr, items.data(), mbytes);
-  SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, sc));
-  SFE_HIP(hipEventRecord(ctx->h_meta.ev, sc));
-  ctx->h_meta.pending = true;
-  const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
-  char* ring = static_cast<char*>(ctx->win.ptr);
-  Source rsrc = src;
-  rsrc.ptr = ring;
-  int32_t norm_first = 0;
-  size_t norm_windows = 0;  // windows featurized since the last normalisation
-  for (size_t bi = 0; bi < batches.size(); ++bi) {
-    const Batch& bt = batches[bi];
-    const int e = (int)(bi & 1);
-    // This half was last read by the log-mel launch of batch bi - 2.
-    if (bi >= 2) SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_done[e], 0));
-    const size_t bytes = (size_t)(bt.end - bt.start) * es;
-    const void* hsrc = host + (size_t)bt.start * es;
-    if (!pinned) {
-      // the pinned staging buffer is free once its previous H2D copy has finished
-      PinBuf& hb = ctx->h_win[e];
-      SFE_HIP(hb.wait());
-      parallel_memcpy(hb.ptr, hsrc, bytes);
-      hsrc = hb.ptr;
-    }
-    SFE_HIP(hipMemcpyAsync(ring + (size_t)e * (size_t)half * es, hsrc, bytes, hipMemcpyHostToDevice, sx));
-    if (!pinned) {
-      SFE_HIP(hipEventRecord(ctx->h_win[e].ev, sx));
-      ctx->h_win[e].pending = true;
-    }
-    SFE_HIP(hipEventRecord(ctx->ev_copied[e], sx));
-    SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[e], 0));
-    const int32_t first = groups[bt.g0].first;
-    const int32_t end = groups[bt.g1 - 1].first + groups[bt.g1 - 1].count;
-    rc = launch_pair(ctx, rsrc, items.data() + first, d_items + first, end - first, raw, out, out_dtype, 0, sc,
-                     kLogmel);
+  return guarded([&]() -> int {
+    const char* host = static_cast<const char*>(host_recording);
+    if (n <= 0 || !tasks || !host || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+    int rc = check_dtype(out_dtype);
     if (rc) return rc;
-    SFE_HIP(hipEventRecord(ctx->ev_done[e], sc));
-    // Normalisation reads only the raw log-mel (all of it stays in HBM), so
-    // it runs once per kStreamNormWindows windows or more instead of per
-    // batch: one launch over many items instead of many launches over a few.
-    norm_windows += bt.g1 - bt.g0;
-    if (bi + 1 == batches.size() || norm_windows >= kStreamNormWindows) {
-      rc = launch_pair(ctx, rsrc, items.data() + norm_first, d_items + norm_first, end - norm_first, raw, out,
-                       out_dtype, 0, sc, kNorm);
-      if (rc) return rc;
-      norm_first = end;
-      norm_windows = 0;
+    Source src;
+    if ((rc = pcm_source(host_recording, pcm_format, bits_per_sample, &src))) return rc;
+    const size_t es = src.esize;
+    std::vector<int64_t> starts(n), lens(n);
+    for (int32_t i = 0; i < n; ++i) {
+      const sfe_chunk& t = tasks[i];
+      if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+        return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+      if (t.audio_end - t.audio_start > window_samples)
+        return fail(SFE_INVALID_ARG, "window_samples is shorter than task " + std::to_string(i));
+      if (i > 0 && t.audio_start < tasks[i - 1].audio_start)
+        return fail(SFE_INVALID_ARG, "tasks must be ordered by audio_start");
+      starts[i] = t.audio_start;
+      lens[i] = t.audio_end - t.audio_start;
     }
-  }
-  SFE_HIP(hipStreamSynchronize(sc));
-  SFE_HIP(hipStreamSynchronize(sx));
-  ctx->has_last = false;  // everything has completed
-  return SFE_OK;
+    if ((rc = check_ctx(ctx))) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    std::vector<Item> items;
+    int64_t tiles = 0;
+    if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
+
+    // Group tasks into windows [wstart, wend) no longer than window_samples;
+    // items are re-based to the window and their tiles to the group.
+    struct Group {
+      int32_t first, count;
+      int64_t wstart, wend;
+      int32_t tiles, max_T;
+    };
+    std::vector<Group> groups;
+    for (int32_t i = 0; i < n;) {
+      Group g{i, 0, items[i].start, items[i].start, 0, 0};
+      while (i < n && items[i].start + items[i].len - g.wstart <= window_samples) {
+        g.wend = std::max(g.wend, items[i].start + items[i].len);
+        ++i;
+        ++g.count;
+      }
+      groups.push_back(g);
+    }
+    // Batches of up to batch_windows consecutive windows.  A batch is copied
+    // as one recording range [start, end) into half (bi & 1) of the device
+    // buffer, so a window joins a batch only while that range stays within
+    // batch_windows * window_samples samples and the gaps between
+    // the batch's windows (copied but unused) add up to at most one window.
+    // Items are re-based to their half and their units numbered within the
+    // batch.
+    struct Batch {
+      size_t g0, g1;
+      int64_t start, end;
+    };
+    const size_t batch_windows =
+        std::min(kStreamMaxBatchWindows, std::max<size_t>(1, kStreamBatchBytes / ((size_t)window_samples * es)));
+    const int64_t half = (int64_t)batch_windows * window_samples;
+    std::vector<Batch> batches;
+    for (size_t gi = 0; gi < groups.size();) {
+      Batch bt{gi, gi + 1, groups[gi].wstart, groups[gi].wend};
+      int64_t covered = groups[gi].wend - groups[gi].wstart;
+      for (++gi; gi < groups.size() && bt.g1 - bt.g0 < batch_windows; ++gi) {
+        const int64_t end = std::max(bt.end, groups[gi].wend);
+        const int64_t cov = covered + (groups[gi].wend - groups[gi].wstart);
+        if (end - bt.start > half || (end - bt.start) - std::min(cov, end - bt.start) > window_samples) break;
+        bt.end = end;
+        covered = cov;
+        bt.g1 = gi + 1;
+      }
+      batches.push_back(bt);
+    }
+    for (size_t bi = 0; bi < batches.size(); ++bi) {
+      const int64_t base = (int64_t)(bi & 1) * half - batches[bi].start;
+      int32_t t = 0;
+      for (size_t gi = batches[bi].g0; gi < batches[bi].g1; ++gi) {
+        Group& g = groups[gi];
+        const int32_t t0 = t;
+        for (int32_t i = g.first; i < g.first + g.count; ++i) {
+          items[i].start += base;
+          items[i].tile_off = t;
+          t += (int32_t)sfe::tiles_for(items[i].T);
+          g.max_T = std::max(g.max_T, (int)items[i].T);
+        }
+        g.tiles = t - t0;
+      }
+    }
+    const size_t mbytes = items.size() * sizeof(Item);
+    ctx->meta_items.clear();  // the table uploaded below is re-based per window group
+    SFE_HIP(ctx->h_meta.reserve(mbytes));
+    SFE_HIP(ctx->meta.reserve(mbytes));
+    SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
+    float* raw = static_cast<float*>(ctx->scratch.ptr);
+    // A recording already in pinned (page-locked) host memory is copied to
+    // the device directly; pageable memory goes through two pinned staging
+    // windows.
+    bool pinned = false;
+    {
+      hipPointerAttribute_t attr;
+      if (hipPointerGetAttributes(&attr, host_recording) == hipSuccess) pinned = attr.type == hipMemoryTypeHost;
+      (void)hipGetLastError();  // a pageable pointer leaves an error code behind
+    }
+    SFE_HIP(ctx->win.reserve(2 * (size_t)half * es));
+    if (!pinned)
+      for (int b = 0; b < 2; ++b) SFE_HIP(ctx->h_win[b].reserve((size_t)half * es));
+    hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
+    if (ctx->has_last) {
+      SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_last, 0));
+      SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_last, 0));
+    }
+    memcpy(ctx->h_meta.ptr, items.data(), mbytes);
+    SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, sc));
+    SFE_HIP(hipEventRecord(ctx->h_meta.ev, sc));
+    ctx->h_meta.pending = true;
+    const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
+    char* ring = static_cast<char*>(ctx->win.ptr);
+    Source rsrc = src;
+    rsrc.ptr = ring;
+    int32_t norm_first = 0;
+    size_t norm_windows = 0;  // windows featurized since the last normalisation
+    for (size_t bi = 0; bi < batches.size(); ++bi) {
+      const Batch& bt = batches[bi];
+      const int e = (int)(bi & 1);
+      // This half was last read by the log-mel launch of batch bi - 2.
+      if (bi >= 2) SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_done[e], 0));
+      const size_t bytes = (size_t)(bt.end - bt.start) * es;
+      const void* hsrc = host + (size_t)bt.start * es;
+      if (!pinned) {
+        // the pinned staging buffer is free once its previous H2D copy has finished
+        PinBuf& hb = ctx->h_win[e];
+        SFE_HIP(hb.wait());
+        parallel_memcpy(hb.ptr, hsrc, bytes);
+        hsrc = hb.ptr;
+      }
+      SFE_HIP(hipMemcpyAsync(ring + (size_t)e * (size_t)half * es, hsrc, bytes, hipMemcpyHostToDevice, sx));
+      if (!pinned) {
+        SFE_HIP(hipEventRecord(ctx->h_win[e].ev, sx));
+        ctx->h_win[e].pending = true;
+      }
+      SFE_HIP(hipEventRecord(ctx->ev_copied[e], sx));
+      SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[e], 0));
+      const int32_t first = groups[bt.g0].first;
+      const int32_t end = groups[bt.g1 - 1].first + groups[bt.g1 - 1].count;
+      rc = launch_pair(ctx, rsrc, items.data() + first, d_items + first, end - first, raw, out, out_dtype, 0, sc,
+                       kLogmel);
+      if (rc) return rc;
+      SFE_HIP(hipEventRecord(ctx->ev_done[e], sc));
+      // Normalisation reads only the raw log-mel (all of it stays in HBM), so
+      // it runs once per kStreamNormWindows windows or more instead of per
+      // batch: one launch over many items instead of many launches over a few.
+      norm_windows += bt.g1 - bt.g0;
+      if (bi + 1 == batches.size() || norm_windows >= kStreamNormWindows) {
+        rc = launch_pair(ctx, rsrc, items.data() + norm_first, d_items + norm_first, end - norm_first, raw, out,
+                         out_dtype, 0, sc, kNorm);
+        if (rc) return rc;
+        norm_first = end;
+        norm_windows = 0;
+      }
+    }
+    SFE_HIP(hipStreamSynchronize(sc));
+    SFE_HIP(hipStreamSynchronize(sx));
+    ctx->has_last = false;  // everything has completed
+    return SFE_OK;
+  });
 }
 
 int sfe_set_timing(sfe_ctx* ctx, int32_t enable) {
@@ -792,22 +835,24 @@ int sfe_set_timing(sfe_ctx* ctx, int32_t enable) {
 }
 
 int sfe_get_timing(sfe_ctx* ctx, double* logmel_ms, double* norm_ms, int32_t* launches) {
-  if (!ctx || !logmel_ms || !norm_ms) return fail(SFE_INVALID_ARG, "null argument");
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  double a = 0.0, b = 0.0;
-  for (size_t i = 0; i + 3 < ctx->tev_used; i += 4) {
-    float t0 = 0.f, t1 = 0.f;
-    SFE_HIP(hipEventSynchronize(ctx->tev[i + 3]));
-    SFE_HIP(hipEventElapsedTime(&t0, ctx->tev[i], ctx->tev[i + 1]));
-    SFE_HIP(hipEventElapsedTime(&t1, ctx->tev[i + 2], ctx->tev[i + 3]));
-    a += t0;
-    b += t1;
-  }
-  *logmel_ms = a;
-  *norm_ms = b;
-  if (launches) *launches = (int32_t)(ctx->tev_used / 4);
-  ctx->tev_used = 0;
-  return SFE_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !logmel_ms || !norm_ms) return fail(SFE_INVALID_ARG, "null argument");
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    double a = 0.0, b = 0.0;
+    for (size_t i = 0; i + 3 < ctx->tev_used; i += 4) {
+      float t0 = 0.f, t1 = 0.f;
+      SFE_HIP(hipEventSynchronize(ctx->tev[i + 3]));
+      SFE_HIP(hipEventElapsedTime(&t0, ctx->tev[i], ctx->tev[i + 1]));
+      SFE_HIP(hipEventElapsedTime(&t1, ctx->tev[i + 2], ctx->tev[i + 3]));
+      a += t0;
+      b += t1;
+    }
+    *logmel_ms = a;
+    *norm_ms = b;
+    if (launches) *launches = (int32_t)(ctx->tev_used / 4);
+    ctx->tev_used = 0;
+    return SFE_OK;
+  });
 }
 
 }  // extern "C"
