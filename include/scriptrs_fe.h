@@ -19,7 +19,9 @@
  * !Sync for the same reason (RefCell workspace, src/frontend.rs:16); calls
  * on one ctx are serialised by an internal mutex.
  * Errors: every entry point returns an sfe_status.  sfe_last_error()
- * returns the calling thread's message for the last failure.
+ * returns the calling thread's message for the last failure.  No C++
+ * exception crosses this interface: a host allocation or thread failure
+ * inside the library returns SFE_HIP_ERROR.
  */
 #ifndef SCRIPTRS_FE_H
 #define SCRIPTRS_FE_H
