@@ -505,3 +505,45 @@ def test_config5_full_streamed_equals_resident(extractor):
         assert np.array_equal(fa, fb)
         assert torch.equal(a, b), dtype
         del a, b
+
+
+def test_contexts_on_concurrent_host_threads():
+    """One context per host thread (the reference's extractor is !Sync, one
+    per worker: src/long_form.rs:288-295): four threads, each with its own
+    extractor and stream, run chunk calls at the same time; every result is
+    bit-identical to a single-threaded run."""
+    import threading
+    import torch
+    from scriptrs_amd import ParakeetFeatureExtractor, build_fast_execution_plan
+    _flush("case: four host threads, one context each")
+    rec = synth.speech_like(2_000_000, 37)
+    tasks = build_fast_execution_plan(rec.size)
+    dev = torch.from_numpy(rec).cuda()
+    ref_ext = ParakeetFeatureExtractor()
+    want, wfo = ref_ext.extract_chunks(dev, tasks)
+    torch.cuda.synchronize()
+    ref_ext.close()
+    results, errors = {}, []
+
+    def work(k):
+        try:
+            ext = ParakeetFeatureExtractor()
+            stream = torch.cuda.Stream()
+            for r in range(5):
+                out, fo = ext.extract_chunks(dev, tasks, stream=stream)
+                stream.synchronize()
+                results[(k, r)] = (out.clone(), fo)
+            ext.close()
+        except Exception as e:  # surfaced below
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=work, args=(k,)) for k in range(4)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert len(results) == 20
+    for (k, r), (out, fo) in results.items():
+        assert np.array_equal(fo, wfo), (k, r)
+        assert torch.equal(out, want), (k, r)
