@@ -466,6 +466,12 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
       const cf src = a[(15 - k2) & 15];
       sh[k2] = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
     }
+    // From here to the pass barrier the wave runs at raised priority: the
+    // workgroup's other waves wait for it at the barrier, so the SIMD's
+    // other wave (another workgroup's) yields to it.  Measured 1.8% faster
+    // on the 1 h workload; starting the raised priority earlier (at the
+    // window or transpose phases) was 5% slower.
+    __builtin_amdgcn_s_setprio(2);
     float* P = pbuf[u & 1][4 * w + g];
 #pragma unroll
     for (int k2 = 0; k2 < 9; ++k2) {
@@ -486,6 +492,7 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
       }
     }
     __syncthreads();  // all 16 power spectra of this pass are in pbuf[u & 1]
+    __builtin_amdgcn_s_setprio(0);
 
     // ---- 3. mel on the matrix cores: D[filter][frame] += W[filter][4 bins] . P[4 bins][frame]
     const float* PB = &pbuf[u & 1][n][kk];
