@@ -2,8 +2,9 @@
 //
 // Host responsibilities: argument validation with the reference's error
 // semantics, per-call item tables (one H2D copy from a pinned staging
-// buffer), device buffer management and stream ordering.  All compute runs
-// in the HIP kernels of sfe_kernels.hip; there is no CPU compute path.
+// buffer), device buffer management, host->device streaming and stream
+// ordering.  All compute runs in the HIP kernels of sfe_kernels.hip and
+// sfe_vad.hip; there is no CPU compute path.
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <string.h>
