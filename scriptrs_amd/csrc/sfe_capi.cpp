@@ -183,6 +183,8 @@ struct sfe_ctx {
   DevBuf scratch;   // raw log-mel, frame-major f32 (the normalisation kernel's input)
   DevBuf io_in;     // sfe_extract staging (audio)
   DevBuf io_out;    // sfe_extract staging (features)
+  PinBuf h_io_in;   // sfe_extract pinned host staging: copies of pageable
+  PinBuf h_io_out;  // memory run as plain memcpy + DMA instead of HIP's own staging
   DevBuf win;       // streamed windows: two halves of one batch each
   PinBuf h_win[2];
   hipEvent_t ev_copied[2] = {nullptr, nullptr};
@@ -480,6 +482,8 @@ void sfe_destroy(sfe_ctx* ctx) {
   ctx->scratch.release();
   ctx->io_in.release();
   ctx->io_out.release();
+  ctx->h_io_in.release();
+  ctx->h_io_out.release();
   ctx->win.release();
   for (int i = 0; i < 2; ++i) {
     ctx->h_win[i].release();
@@ -503,17 +507,22 @@ int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64
     const int64_t T = len / sfe::kHop + 1;
     const int64_t nout = T * sfe::kMel;
     if (out_capacity < nout) return fail(SFE_INVALID_ARG, "output buffer too small");
-    SFE_HIP(ctx->io_in.reserve((size_t)len * sizeof(float)));
-    SFE_HIP(ctx->io_out.reserve((size_t)nout * sizeof(float)));
+    const size_t in_bytes = (size_t)len * sizeof(float), out_bytes = (size_t)nout * sizeof(float);
+    SFE_HIP(ctx->io_in.reserve(in_bytes));
+    SFE_HIP(ctx->io_out.reserve(out_bytes));
+    SFE_HIP(ctx->h_io_in.reserve(in_bytes));
+    SFE_HIP(ctx->h_io_out.reserve(out_bytes));
     hipStream_t s = ctx->s_compute;
-    SFE_HIP(hipMemcpyAsync(ctx->io_in.ptr, audio, (size_t)len * sizeof(float), hipMemcpyHostToDevice, s));
+    parallel_memcpy(ctx->h_io_in.ptr, audio, in_bytes);
+    SFE_HIP(hipMemcpyAsync(ctx->io_in.ptr, ctx->h_io_in.ptr, in_bytes, hipMemcpyHostToDevice, s));
     std::vector<Item> items;
     int64_t start = 0, tiles = 0, fo[2];
     if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
     if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
       return rc;
-    SFE_HIP(hipMemcpyAsync(out, ctx->io_out.ptr, (size_t)nout * sizeof(float), hipMemcpyDeviceToHost, s));
+    SFE_HIP(hipMemcpyAsync(ctx->h_io_out.ptr, ctx->io_out.ptr, out_bytes, hipMemcpyDeviceToHost, s));
     SFE_HIP(hipStreamSynchronize(s));
+    parallel_memcpy(out, ctx->h_io_out.ptr, out_bytes);
     return SFE_OK;
   });
 }
