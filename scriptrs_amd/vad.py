@@ -57,7 +57,8 @@ class SileroVadFramer:
             raise InvalidModelOutput("out must be a float32 tensor of at least n_windows x 576 elements")
         if n == 0:
             return out
-        rc = _lib.lib().sfe_vad_frames(self._fe._handle(), _dev_ptr(recording), pcm, bits, recording.numel(),
-                                       _dev_ptr(out), out.numel() // VAD_INPUT_SAMPLES, _stream_handle(stream))
+        rec_ptr, out_ptr = _dev_ptr(recording), _dev_ptr(out)  # checked before any device work
+        rc = _lib.lib().sfe_vad_frames(self._fe._handle(), rec_ptr, pcm, bits, recording.numel(), out_ptr,
+                                       out.numel() // VAD_INPUT_SAMPLES, _stream_handle(stream))
         _check(rc)
         return out

@@ -1,0 +1,64 @@
+"""Python host helpers without a GPU: the task table in the C ABI layout,
+the sample-format mapping, and argument checks that run before any device
+work."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from scriptrs_amd import (ChunkTask, InvalidModelOutput, SileroVadFramer, TaskTable, build_fast_execution_plan,
+                          vad_num_windows)
+from scriptrs_amd import _lib
+from scriptrs_amd.frontend import _dtype_code, _pcm_format
+
+
+def test_task_table_matches_the_c_layout():
+    tasks = build_fast_execution_plan(57_600_000)
+    tt = TaskTable(tasks)
+    assert tt.n == len(tt) == 280
+    assert tt.array.dtype == np.int64 and tt.array.shape == (280, 4)
+    # same bytes the ctypes struct array would hold
+    assert ctypes.sizeof(_lib.SfeChunk) == 32
+    first = tt.ptr[0]
+    assert (first.audio_start, first.audio_end, first.global_sample_offset, first.context_samples) == \
+        (tasks[0].audio_start, tasks[0].audio_end, tasks[0].global_sample_offset, tasks[0].context_samples)
+    last = tt.ptr[279]
+    assert (last.audio_start, last.audio_end) == (tasks[-1].audio_start, tasks[-1].audio_end)
+    assert int(tt.frame_offsets[-1]) == 418_312
+    assert np.array_equal(np.diff(tt.frame_offsets), (tt.array[:, 1] - tt.array[:, 0]) // 160 + 1)
+
+
+def test_task_table_from_array_and_empty():
+    a = np.array([[0, 160, 0, 0], [100, 420, 100, 0]], np.int64)
+    tt = TaskTable(a)
+    assert list(tt.frame_offsets) == [0, 2, 5]  # 160 samples: 2 frames; 320: 3
+    tt2 = TaskTable([ChunkTask(0, 160, 0, 0), ChunkTask(100, 420, 100, 0)])
+    assert np.array_equal(tt.array, tt2.array)
+    with pytest.raises(InvalidModelOutput):
+        TaskTable([])
+
+
+@pytest.mark.parametrize("dtype,bits,want", [("float32", None, (0, 32)), ("int16", None, (1, 16)),
+                                             ("int16", 12, (1, 12)), ("int32", None, (2, 32)),
+                                             ("int32", 24, (2, 24)), ("torch.int16", None, (1, 16))])
+def test_pcm_format(dtype, bits, want):
+    assert _pcm_format(dtype, bits) == want
+
+
+def test_pcm_format_and_dtype_errors():
+    with pytest.raises(InvalidModelOutput):
+        _pcm_format("float64", None)
+    with pytest.raises(InvalidModelOutput):
+        _dtype_code("f16")
+    assert _dtype_code("f32") == _lib.SFE_F32 and _dtype_code("bf16") == _lib.SFE_BF16
+
+
+def test_vad_framer_rejects_host_tensors_and_small_outputs():
+    import torch
+    f = SileroVadFramer()
+    with pytest.raises(InvalidModelOutput, match="device tensor"):
+        f.model_inputs(torch.zeros(1000))
+    with pytest.raises(InvalidModelOutput, match="at least"):
+        f.model_inputs(torch.zeros(1000), out=torch.zeros((1, 576)))
+    assert vad_num_windows(1000) == 2
+    f.close()
