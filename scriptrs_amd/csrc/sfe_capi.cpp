@@ -180,7 +180,7 @@ struct sfe_ctx {
   hipEvent_t ev_last = nullptr;
   bool has_last = false;
   PinBuf h_meta;
-  DevBuf scratch;   // raw log-mel, frame-major f32 (the normalisation kernel's input)
+  DevBuf scratch;   // raw log-mel in 16-frame tiles, f32 (the normalisation kernel's input)
   DevBuf io_in;     // sfe_extract staging (audio)
   DevBuf io_out;    // sfe_extract staging (features)
   PinBuf h_io_in;   // sfe_extract pinned host staging: copies of pageable
@@ -210,8 +210,8 @@ int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vect
     Item& it = (*items)[i];
     it.start = starts[i];
     it.len = lens[i];
-    it.out_off = (int64_t)sfe::kMel * fo;
-    it.dst_off = it.out_off;
+    it.out_off = (int64_t)sfe::kRawTile * tiles;  // raw scratch: whole 16-frame tiles per item
+    it.dst_off = (int64_t)sfe::kMel * fo;
     it.T = (int32_t)T;
     it.tile_off = (int32_t)tiles;
     fo += T;
@@ -270,7 +270,7 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* 
 // Uploads items through the pinned staging buffer on `stream`, then runs
 // the log-mel and normalisation kernels.
 int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, int64_t total_tiles,
-              int64_t total_frames, int32_t out_dtype, void* out, hipStream_t stream, int pad_to = 0) {
+              int32_t out_dtype, void* out, hipStream_t stream, int pad_to = 0) {
   if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(stream, ctx->ev_last, 0));
   const size_t mbytes = items.size() * sizeof(Item);
   // A call with the same item table as the previous upload (repeated plans,
@@ -289,9 +289,8 @@ int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, i
     ctx->meta_items = items;
   }
   const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
-  SFE_HIP(ctx->scratch.reserve((size_t)total_frames * sfe::kMel * sizeof(float)));
+  SFE_HIP(ctx->scratch.reserve((size_t)total_tiles * sfe::kRawTile * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
-  (void)total_tiles;
   const int rc = launch_pair(ctx, src, items.data(), d_items, (int)items.size(), raw, out, out_dtype, pad_to, stream);
   if (rc) return rc;
   SFE_HIP(hipEventRecord(ctx->ev_last, stream));
@@ -518,7 +517,7 @@ int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64
     std::vector<Item> items;
     int64_t start = 0, tiles = 0, fo[2];
     if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
-    if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, T, SFE_F32, ctx->io_out.ptr, s)))
+    if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, SFE_F32, ctx->io_out.ptr, s)))
       return rc;
     SFE_HIP(hipMemcpyAsync(ctx->h_io_out.ptr, ctx->io_out.ptr, out_bytes, hipMemcpyDeviceToHost, s));
     SFE_HIP(hipStreamSynchronize(s));
@@ -562,7 +561,7 @@ int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets
     std::vector<Item> items;
     int64_t tiles = 0;
     if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-    return run_items(ctx, f32_source(samples), items, tiles, frame_offsets[n], out_dtype, out,
+    return run_items(ctx, f32_source(samples), items, tiles, out_dtype, out,
                      static_cast<hipStream_t>(stream));
   });
 }
@@ -594,7 +593,7 @@ int sfe_extract_chunks_pcm(sfe_ctx* ctx, const void* recording, int32_t pcm_form
     std::vector<Item> items;
     int64_t tiles = 0;
     if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-    return run_items(ctx, src, items, tiles, frame_offsets[n], out_dtype, out, static_cast<hipStream_t>(stream));
+    return run_items(ctx, src, items, tiles, out_dtype, out, static_cast<hipStream_t>(stream));
   });
 }
 
@@ -628,7 +627,7 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
       items[i].dst_off = (int64_t)i * sfe::kMel * target_frames;
       feature_frames[i] = items[i].T;
     }
-    return run_items(ctx, f32_source(recording), items, tiles, fo[n], out_dtype, out, static_cast<hipStream_t>(stream),
+    return run_items(ctx, f32_source(recording), items, tiles, out_dtype, out, static_cast<hipStream_t>(stream),
                      target_frames);
   });
 }
@@ -761,7 +760,7 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     ctx->meta_items.clear();  // the table uploaded below is re-based per window group
     SFE_HIP(ctx->h_meta.reserve(mbytes));
     SFE_HIP(ctx->meta.reserve(mbytes));
-    SFE_HIP(ctx->scratch.reserve((size_t)frame_offsets[n] * sfe::kMel * sizeof(float)));
+    SFE_HIP(ctx->scratch.reserve((size_t)tiles * sfe::kRawTile * sizeof(float)));
     float* raw = static_cast<float*>(ctx->scratch.ptr);
     // A recording already in pinned (page-locked) host memory is copied to
     // the device directly; pageable memory goes through two pinned staging

@@ -38,12 +38,15 @@ static_assert(wave_steps(0) <= kMaxSteps && wave_steps(1) <= kMaxSteps && wave_s
 
 // One featurized item: a clip or a long-form chunk task.  samples[start,
 // start+len) is featurized into out[dst_off + m*S + t] (S = T, or the
-// padded row length of the encoder-input layout; raw log-mel in
-// scratch at raw[out_off + t*128 + m], as log2; times ln 2 is the log-mel).
+// padded row length of the encoder-input layout).  The raw log-mel (log2;
+// times ln 2 is the log-mel) goes to scratch in tiles of 16 frames: tile
+// t / 16 of the item at raw[out_off + 2048 * (t / 16)], holding 8 slabs of
+// 16 features, each [16 frames][16 features] (the slab order inside the tile
+// is the log-mel kernel's kSlabPos).
 struct Item {
   int64_t start;
   int64_t len;
-  int64_t out_off;   // raw (scratch) element offset = feature_size * frame_offset
+  int64_t out_off;   // raw (scratch) element offset: kRawTile * (tiles of the items before it)
   int64_t dst_off;   // output element offset: out_off when packed, i * feature_size * pad_to when padded
   int32_t T;         // len / hop + 1
   int32_t tile_off;  // first 16-frame unit of this item, relative to the launch
@@ -69,6 +72,7 @@ bool build_dev_tables(int sample_rate, DevTables* t);
 
 // Kernel launchers (sfe_kernels.hip).  All asynchronous on `stream`.
 constexpr int kTile = 16;  // frames per unit of work (one pass) of the log-mel kernel
+constexpr int kRawTile = kTile * 128;  // raw scratch floats per tile of 16 frames
 int64_t tiles_for(int64_t T);
 // grid_cap: workgroups resident on the device at once (the kernel loops
 // over tiles, so launching more than that only adds scheduling overhead).
@@ -83,7 +87,7 @@ hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const It
                          hipStream_t stream);
 constexpr int kLogmelWavesPerSimd = 2;
 constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
-// Normalises raw (f32 log2 values, frame-major [T][128] per item) per (item, feature)
+// Normalises raw (f32 log2 values in 16-frame tiles, see Item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
 // frame count (sizes the kernel's register budget).  pad_to > 0: rows of

@@ -6,8 +6,9 @@
 //   preemphasis restarted at the item start -> 256-zero padding ->
 //   400-tap left-aligned Hann window -> 512-point real FFT -> |X|^2 ->
 //   128x257 Slaney mel contraction -> ln(x + 2^-24)
-// and writes the raw log-mel frame-major ([T][128] per item) to scratch, in
-// base 2 (the normalisation kernel multiplies by ln 2 as it loads).
+// and writes the raw log-mel to scratch in tiles of 16 frames (8 slabs of 16
+// features, frame-major inside each slab), in base 2 (the normalisation
+// kernel multiplies by ln 2 as it loads).
 // sfe_norm_kernel then applies normalize_columns (src/frontend.rs:225-241)
 // per (item, feature) and writes the reference's feature-major layout
 // ([128][T] per item).
@@ -242,11 +243,19 @@ __device__ __forceinline__ void mel_mfma(const float (&av)[kMaxSteps], const int
   }
 }
 
-// Raw log-mel is written frame-major ([T][128] per item): lane (n, kk)
-// holds filters 16 b + 4 kk .. + 3 of frame n, one aligned 16-byte store.
-// The 4 waves of a pass together cover whole 512-byte frame rows.
+// Raw log-mel is written in tiles of 16 frames (one pass): 8 slabs of 16
+// features, each slab [16 frames][16 features] (1 KB).  Lane (n, kk) holds
+// filters 16 b + 4 kk .. + 3 of frame n: one aligned 16-byte store, and one
+// store instruction writes a whole contiguous slab.  The normalisation
+// kernel, which works per (item, slab), then reads 1 KB contiguous per load
+// instruction.  (Frame-major [T][128] rows made it read 64-byte pieces:
+// 0.095 ms against 0.079 ms for the 1 h workload; this layout costs log-mel
+// 2%.)  Slabs sit in the tile in the order of the waves' filter blocks
+// (kWaveBlocks: 7 | 6 | 5 3 0 | 4 2 1), so each wave's stores are
+// adjacent and share one base address.
+constexpr int kSlabPos[kBlocks] = {4, 7, 6, 3, 5, 2, 1, 0};
 __device__ __forceinline__ void store_block(const f32x4& v, int b, float* frame_row, int kk) {
-  *reinterpret_cast<float4*>(frame_row + 16 * b + 4 * kk) =
+  *reinterpret_cast<float4*>(frame_row + 256 * kSlabPos[b] + 4 * kk) =
       make_float4(guarded_log2(v[0]), guarded_log2(v[1]), guarded_log2(v[2]), guarded_log2(v[3]));
 }
 
@@ -504,7 +513,7 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
     }
     const int t = f0 + n;
     pend = t < T;
-    pend_row = o + (int64_t)(pend ? t : 0) * kMel;
+    pend_row = o + (int64_t)kRawTile * (u - it.tile_off) + 16 * n;  // this pass's tile, frame n's slab rows
   }
   store_pending(w, acc, pend_row, pend, kk);
 }
@@ -534,8 +543,8 @@ __device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_
   *sd_out = __fsqrt_rn(var) + 1e-5f;
 }
 
-// normalize_columns (src/frontend.rs:225-241).  Input: raw log-mel,
-// frame-major ([T][128] per item, as the log-mel kernel writes it).
+// normalize_columns (src/frontend.rs:225-241).  Input: raw log-mel in
+// 16-frame tiles of 8 slabs (as the log-mel kernel writes it).
 // Output: feature-major ([128][T] per item, the reference's memory order).
 //
 // One workgroup of W waves per (item, slab of F features).  Loads: in round
@@ -745,12 +754,15 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   const int slab = (work % S::kSlabs) * F;
   const Item it = items[item];
   const int T = it.T;
-  // Uniform bases with 32-bit lane offsets.
-  const float* xb = raw + it.out_off + slab;
+  // Uniform bases with 32-bit lane offsets.  Raw tiles hold 16 frames, each
+  // slab 1 KB frame-major inside (kSlabPos): frame f of this slab sits at
+  // xb + kRawTile * (f / 16) + 16 * (f % 16).
+  static_assert(F == 16 && S::kGroup == 16, "one wave's load covers one tile of one slab");
+  const float* xb = raw + it.out_off + 256 * kSlabPos[slab / 16];
   const int rs = pad_to > 0 ? pad_to : T;  // output row length
   O* ob = out + it.dst_off + (size_t)slab * rs;
   if (pad_to > 0) zero_tail<W, F>(ob, T, rs, lane, w);
-  const uint32_t lo = (uint32_t)(fr * kMel + 4 * q);
+  const uint32_t lo = (uint32_t)((fr / 16) * kRawTile + (fr % 16) * 16 + 4 * q);
   const int nr = fr < T ? (T - 1 - fr) / kSpan + 1 : 0;  // rounds holding a frame of this lane
   const float4 x0 = ln2_scale(*reinterpret_cast<const float4*>(xb + 4 * q));
 
@@ -764,7 +776,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
       // branch waits for itself, and the rounds would load one at a time.
 #pragma unroll
       for (int j = 0; j < N; ++j) {
-        const size_t off = j < nr ? (size_t)j * (kSpan * kMel) + lo : (size_t)lo;
+        const size_t off = j < nr ? (size_t)j * (kSpan / 16 * kRawTile) + lo : (size_t)lo;
         v[j] = *reinterpret_cast<const float4*>(xb + (nr > 0 ? off : (size_t)(4 * q)));
       }
 #pragma unroll
@@ -823,7 +835,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int j = j0 + g < nr ? j0 + g : j0;  // in bounds; unused when past the item
-      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
+      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan / 16 * kRawTile) + lo));
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -848,7 +860,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int j = j0 + g < nr ? j0 + g : j0;  // in bounds; unused when past the item
-      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan * kMel) + lo));
+      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan / 16 * kRawTile) + lo));
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -870,7 +882,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     for (int jr = 0; jr < 4; ++jr) {
       // past the item: the item's first frame (always in bounds), unused
       const int j = 4 * ch + jr;
-      e[jr] = ln2_scale(*reinterpret_cast<const float4*>(xb + (j < nr ? (size_t)j * (kSpan * kMel) + lo : (size_t)(4 * q))));
+      e[jr] = ln2_scale(*reinterpret_cast<const float4*>(xb + (j < nr ? (size_t)j * (kSpan / 16 * kRawTile) + lo : (size_t)(4 * q))));
     }
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr)
@@ -881,23 +893,16 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   }
 }
 
-// Workgroups of kNormMainWaves waves over 16-feature slabs, two per CU.
-// The two slabs of one 128-byte frame line go to workgroups 8 apart, which
-// the dispatcher places on the same XCD (round-robin over the 8 XCDs), so
-// the second half-line read hits that XCD's L2.
+// Workgroups of kNormMainWaves waves over 16-feature slabs, three per CU;
+// workgroup b normalises slab b % 8 of item b / 8.
 constexpr int kNormMainWaves = 4;
 constexpr int kNormMainSlab = 16;
-
-__device__ __forceinline__ int xcd_pair_work(int b) {
-  // b = 16 k + 8 h + x  ->  work 16 k + 2 x + h
-  return (b & ~15) + 2 * (b & 7) + ((b >> 3) & 1);
-}
 
 template <int N, typename O>
 __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const float* __restrict__ raw,
                                                                        const Item* __restrict__ items, int n_items,
                                                                        int pad_to, O* __restrict__ out) {
-  norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, xcd_pair_work(blockIdx.x), pad_to, out);
+  norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, blockIdx.x, pad_to, out);
 }
 
 }  // namespace
@@ -927,8 +932,7 @@ template <typename O>
 hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int max_T, int pad_to, O* out,
                          hipStream_t stream) {
   using S = NormShape<kNormMainWaves, kNormMainSlab>;
-  // whole groups of 16 workgroups (xcd_pair_work); the extra ones exit
-  const unsigned blocks = (unsigned)(((int64_t)n_items * S::kSlabs + 15) / 16 * 16);
+  const unsigned blocks = (unsigned)((int64_t)n_items * S::kSlabs);
   const dim3 grid(blocks), block(S::kThreads);
   // Registers per lane sized to the longest item (N float4s hold kSpan N
   // frames); longer items take the streaming path.
