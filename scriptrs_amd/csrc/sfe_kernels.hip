@@ -373,8 +373,6 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
 #pragma unroll
     for (int h = 0; h < kSpanVec; ++h) cv[h] = Pcm<S>::dec4(nv[h], dc);
     const float cxm1 = Pcm<S>::dec(nxm1, dc);
-    const int T = it.T;
-    const int f0 = (u - it.tile_off) * kPassFrames;
     float* o = out + it.out_off;
 
     // ---- 1. preemphasised, zero-padded samples of this wave's 4 frames
@@ -511,8 +509,9 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
       case 2: mel_mfma<2>(av, k0b, PB, acc); break;
       default: mel_mfma<3>(av, k0b, PB, acc); break;
     }
-    const int t = f0 + n;
-    pend = t < T;
+    // Every frame of the pass is stored: frames past the item's end land in
+    // its last tile's padding, which nothing reads (1% faster than masking).
+    pend = true;
     pend_row = o + (int64_t)kRawTile * (u - it.tile_off) + 16 * n;  // this pass's tile, frame n's slab rows
   }
   store_pending(w, acc, pend_row, pend, kk);
