@@ -93,8 +93,8 @@ def make_workload(name: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="config3", choices=["config1", "config1host", "config2", "config3", "config4", "config5", "vad1h"])
     ap.add_argument("--pcm", default="f32", choices=["f32", "i16"],
                     help="input samples: f32, or 16-bit PCM decoded in the kernel")
