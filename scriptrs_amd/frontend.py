@@ -110,11 +110,36 @@ def _stream_handle(stream) -> ctypes.c_void_p:
 
 
 def _dev_ptr(t) -> ctypes.c_void_p:
-    if not t.is_cuda:
+    if not getattr(t, "is_cuda", False):
         raise InvalidModelOutput("expected a device tensor")
     if not t.is_contiguous():
         raise InvalidModelOutput("expected a contiguous tensor")
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _torch_dtype(dtype: str):
+    import torch
+    _dtype_code(dtype)
+    return torch.float32 if dtype == "f32" else torch.bfloat16
+
+
+def _check_samples(t, *dtypes) -> None:
+    """The C ABI reads ``numel`` samples of the element size its format
+    implies; a tensor of another dtype would be read past its end."""
+    _dev_ptr(t)
+    if t.dtype not in dtypes:
+        raise InvalidModelOutput(f"samples must be {' or '.join(str(d) for d in dtypes)}, got {t.dtype}")
+
+
+def _check_out(out, dtype: str, numel: int) -> None:
+    """A caller-supplied output must have the requested dtype and room for
+    every element the kernels write."""
+    _dev_ptr(out)
+    want = _torch_dtype(dtype)
+    if out.dtype != want:
+        raise InvalidModelOutput(f"out must be {want} for dtype {dtype!r}, got {out.dtype}")
+    if out.numel() < numel:
+        raise InvalidModelOutput(f"out holds {out.numel()} elements, {numel} needed")
 
 
 class ParakeetFeatureExtractor:
@@ -168,23 +193,29 @@ class ParakeetFeatureExtractor:
         return out.T
 
     # -- batched entry points (one GPU launch sequence) ---------------------------
-    def extract_batch(self, samples, offsets: Sequence[int], dtype: str = "f32", stream=None):
+    def extract_batch(self, samples, offsets: Sequence[int], dtype: str = "f32", stream=None, out=None):
         """Featurize clips ``samples[offsets[i]:offsets[i+1]]`` of a device tensor.
 
         Returns ``(out, frame_offsets)``: ``out`` is a flat device tensor of
         ``128 * sum(T_i)`` elements, clip ``i`` at ``out[128*fo[i]:128*fo[i+1]]``
         viewed as [128, T_i].  Each clip matches one ``extract`` call."""
         import torch
-        off = np.ascontiguousarray(offsets, np.int64)
+        _check_samples(samples, torch.float32)
+        off = np.ascontiguousarray(offsets, np.int64).reshape(-1)
         n = off.size - 1
         if n <= 0:
             raise InvalidModelOutput("need at least one clip")
+        if off[0] < 0 or np.any(np.diff(off) < 0):
+            raise InvalidModelOutput("offsets must be non-negative and non-decreasing")
+        if off[-1] > samples.numel():
+            raise InvalidModelOutput(f"offsets run to {int(off[-1])}, past the {samples.numel()} samples")
         if np.any(np.diff(off) == 0):
             raise EmptyAudio()
         fo = np.zeros(n + 1, np.int64)
         fo[1:] = np.cumsum(np.diff(off) // self.config.hop_length + 1)
-        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-        out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=samples.device)
+        if out is None:
+            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=_torch_dtype(dtype), device=samples.device)
+        _check_out(out, dtype, int(fo[-1]) * self.config.feature_size)
         rc = _lib.lib().sfe_extract_batch(self._handle(), _dev_ptr(samples), _ip(off), n, _dtype_code(dtype),
                                           _dev_ptr(out), _ip(fo), _stream_handle(stream))
         _check(rc)
@@ -195,12 +226,13 @@ class ParakeetFeatureExtractor:
         copying the overlaps (replaces the per-task ``ChunkPreparer::prepare``
         calls of src/long_form.rs:584-592)."""
         import torch
+        _check_samples(recording, torch.float32)
         tt = _tasks_array(tasks, self.config.hop_length)
         arr, n = tt.ptr, tt.n
         fo = tt.frame_offsets.copy()
-        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
-            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=recording.device)
+            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=_torch_dtype(dtype), device=recording.device)
+        _check_out(out, dtype, int(fo[-1]) * self.config.feature_size)
         rc = _lib.lib().sfe_extract_chunks(self._handle(), _dev_ptr(recording), recording.numel(), arr, n,
                                            _dtype_code(dtype), _dev_ptr(out), _ip(fo), _stream_handle(stream))
         _check(rc)
@@ -214,13 +246,14 @@ class ParakeetFeatureExtractor:
         (examples/transcribe_wav.rs:342-348).  ``bits_per_sample`` defaults to
         the container width."""
         import torch
+        _check_samples(recording, torch.float32, torch.int16, torch.int32)
         pcm, bits = _pcm_format(recording.dtype, bits_per_sample)
         tt = _tasks_array(tasks, self.config.hop_length)
         arr, n = tt.ptr, tt.n
         fo = tt.frame_offsets.copy()
-        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
-            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=recording.device)
+            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=_torch_dtype(dtype), device=recording.device)
+        _check_out(out, dtype, int(fo[-1]) * self.config.feature_size)
         rc = _lib.lib().sfe_extract_chunks_pcm(self._handle(), _dev_ptr(recording), pcm, bits, recording.numel(), arr,
                                                n, _dtype_code(dtype), _dev_ptr(out), _ip(fo), _stream_handle(stream))
         _check(rc)
@@ -235,13 +268,14 @@ class ParakeetFeatureExtractor:
         to ``max_feature_frames()`` (``PreparedChunk::target_frames``,
         src/pipeline.rs:160-163).  Returns ``(out, feature_frames)``."""
         import torch
+        _check_samples(recording, torch.float32)
         tt = _tasks_array(tasks, self.config.hop_length)
         arr, n = tt.ptr, tt.n
         tf = int(target_frames or self.config.max_feature_frames())
         ff = np.zeros(n, np.int64)
-        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
-            out = torch.empty((n, self.config.feature_size, tf), dtype=tdt, device=recording.device)
+            out = torch.empty((n, self.config.feature_size, tf), dtype=_torch_dtype(dtype), device=recording.device)
+        _check_out(out, dtype, n * self.config.feature_size * tf)
         rc = _lib.lib().sfe_extract_chunks_padded(self._handle(), _dev_ptr(recording), recording.numel(), arr, n, tf,
                                                   _dtype_code(dtype), _dev_ptr(out), _ip(ff), _stream_handle(stream))
         _check(rc)
@@ -261,9 +295,10 @@ class ParakeetFeatureExtractor:
         tt = _tasks_array(tasks, self.config.hop_length)
         arr, n = tt.ptr, tt.n
         fo = tt.frame_offsets.copy()
-        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         if out is None:
-            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=tdt, device=f"cuda:{self.device}")
+            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=_torch_dtype(dtype),
+                              device=f"cuda:{self.device}")
+        _check_out(out, dtype, int(fo[-1]) * self.config.feature_size)
         rc = _lib.lib().sfe_extract_chunks_streamed_pcm(self._handle(), h.ctypes.data_as(ctypes.c_void_p), pcm, bits,
                                                         h.size, arr, n, _dtype_code(dtype), _dev_ptr(out), _ip(fo),
                                                         int(window_samples))

@@ -62,3 +62,57 @@ def test_vad_framer_rejects_host_tensors_and_small_outputs():
         f.model_inputs(torch.zeros(1000), out=torch.zeros((1, 576)))
     assert vad_num_windows(1000) == 2
     f.close()
+
+
+class _FakeDeviceTensor:
+    """Stands in for a device tensor so the argument checks that run before
+    any GPU call can be exercised without a GPU."""
+
+    def __init__(self, numel, dtype):
+        self._n, self.dtype, self.is_cuda, self.device = numel, dtype, True, "cuda:0"
+
+    def numel(self):
+        return self._n
+
+    def is_contiguous(self):
+        return True
+
+    def data_ptr(self):
+        return 0
+
+
+def test_batched_entry_points_validate_buffers_before_the_c_call():
+    import torch
+    from scriptrs_amd import ParakeetFeatureExtractor
+    ext = ParakeetFeatureExtractor()
+    f32, i16 = torch.float32, torch.int16
+    tasks = [ChunkTask(0, 1600, 0, 0)]  # 11 frames
+    good = _FakeDeviceTensor(128 * 11, f32)
+    # samples of the wrong dtype would be read as 4-byte samples past their end
+    with pytest.raises(InvalidModelOutput, match="samples must be"):
+        ext.extract_chunks(_FakeDeviceTensor(1600, i16), tasks, out=good)
+    with pytest.raises(InvalidModelOutput, match="samples must be"):
+        ext.extract_batch(_FakeDeviceTensor(1600, i16), [0, 1600], out=good)
+    with pytest.raises(InvalidModelOutput, match="samples must be"):
+        ext.extract_chunks_encoder_input(_FakeDeviceTensor(1600, torch.float64), tasks, out=good)
+    # offsets past the buffer (the C ABI has no length to check them against)
+    with pytest.raises(InvalidModelOutput, match="past the"):
+        ext.extract_batch(_FakeDeviceTensor(1599, f32), [0, 1600], out=good)
+    with pytest.raises(InvalidModelOutput, match="non-decreasing"):
+        ext.extract_batch(_FakeDeviceTensor(3200, f32), [0, 1600, 800], out=good)
+    # a caller-supplied output of the wrong dtype or too small
+    with pytest.raises(InvalidModelOutput, match="out must be"):
+        ext.extract_chunks(_FakeDeviceTensor(1600, f32), tasks, out=_FakeDeviceTensor(128 * 11, torch.bfloat16))
+    with pytest.raises(InvalidModelOutput, match="elements"):
+        ext.extract_chunks(_FakeDeviceTensor(1600, f32), tasks, out=_FakeDeviceTensor(128 * 11 - 1, f32))
+    with pytest.raises(InvalidModelOutput, match="elements"):
+        ext.extract_chunks_pcm(_FakeDeviceTensor(1600, i16), tasks, dtype="bf16",
+                               out=_FakeDeviceTensor(128 * 10, torch.bfloat16))
+    with pytest.raises(InvalidModelOutput, match="elements"):
+        ext.extract_batch(_FakeDeviceTensor(1600, f32), [0, 1600], out=_FakeDeviceTensor(100, f32))
+    with pytest.raises(InvalidModelOutput, match="elements"):
+        ext.extract_chunks_encoder_input(_FakeDeviceTensor(1600, f32), tasks, target_frames=1501,
+                                         out=_FakeDeviceTensor(128 * 1500, f32))
+    with pytest.raises(InvalidModelOutput, match="device tensor"):
+        ext.extract_chunks(torch.zeros(1600), tasks, out=good)
+    assert not ext._ctx  # nothing above reached the GPU
