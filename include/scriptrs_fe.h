@@ -188,6 +188,23 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
                               int32_t target_frames, int32_t out_dtype, void* out, int64_t* feature_frames,
                               void* stream);
 
+/* Allocation-free variant of sfe_extract_chunks.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It runs the same kernels as sfe_extract_chunks, with the same
+ * results, but keeps its item table and raw log-mel in a static device array
+ * of the library (one per GPU, held until the process ends) instead of the
+ * context's growable buffers, and calls no hipMalloc, hipFree or other
+ * allocating routine.  Limits: at most 4096 tasks, and at most 64 MiB of raw
+ * log-mel, which is 8192 tiles of 16 frames per task rounded up (131,072
+ * frames, about 22 minutes of audio in 15 s chunks); larger calls return
+ * SFE_INVALID_ARG.  Every call on one GPU shares that array, from every
+ * context: calls that overlap on one GPU (several host threads or contexts
+ * on one device without ordering between them) race.  Calls on one context
+ * are ordered.  Arguments, outputs and errors as sfe_extract_chunks. */
+int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
+                               int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream);
+
 /* Silero VAD model inputs.  Replaces the framing half of the reference's
  * VAD loop (process_coreml_vad, src/long_form/vad.rs:62-99; window 512 and
  * context 64 samples, src/constants.rs:6-11): for each 512-sample window w

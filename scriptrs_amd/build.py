@@ -30,6 +30,7 @@ SOURCES = [
     # (source, extra flags)
     ("sfe_kernels.hip", ["-x", "hip"]),
     ("sfe_vad.hip", ["-x", "hip"]),
+    ("sfe_noalloc.hip", ["-x", "hip"]),
     # bit-exact table construction: every f32/f64 op rounded separately
     ("sfe_tables.cpp", ["-x", "hip", "-ffp-contract=off"]),
     ("sfe_capi.cpp", ["-x", "hip"]),

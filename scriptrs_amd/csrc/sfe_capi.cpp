@@ -193,6 +193,10 @@ struct sfe_ctx {
   bool timing = false;
   std::vector<hipEvent_t> tev;  // pairs: start, end; kind alternates logmel, norm
   size_t tev_used = 0;
+  // This device's static scratch (sfe_extract_chunks_noalloc): item table,
+  // then raw log-mel.  Looked up at creation; h_meta is reserved for its
+  // largest item table at creation too.
+  unsigned char* noalloc = nullptr;
 };
 
 namespace {
@@ -245,14 +249,15 @@ hipEvent_t timing_event(sfe_ctx* ctx) {
 enum Stages { kLogmel = 1, kNorm = 2, kBoth = 3 };
 
 int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d_items, int n, float* raw,
-                void* out, int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth) {
+                void* out, int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth,
+                bool allow_timing = true) {
   if (n <= 0) return SFE_OK;
   const int u0 = items[0].tile_off;
   const int u1 = items[n - 1].tile_off + (int)sfe::tiles_for(items[n - 1].T);
   int max_T = 0;
   for (int i = 0; i < n; ++i) max_T = std::max(max_T, (int)items[i].T);
   hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
-  if (ctx->timing)
+  if (ctx->timing && allow_timing)
     for (int i = 0; i < 4; ++i)
       if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
   if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
@@ -460,6 +465,11 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
       return cleanup(hip_fail(e, "hipStreamCreate"));
     if ((e = hipEventCreateWithFlags(&ctx->ev_last, hipEventDisableTiming)) != hipSuccess)
       return cleanup(hip_fail(e, "hipEventCreate"));
+    void* na = nullptr;
+    if ((e = sfe::noalloc_scratch(device, &na)) != hipSuccess) return cleanup(hip_fail(e, "hipGetSymbolAddress(scratch)"));
+    ctx->noalloc = static_cast<unsigned char*>(na);
+    if ((e = ctx->h_meta.reserve((size_t)sfe::kNoAllocMaxItems * sizeof(Item))) != hipSuccess)
+      return cleanup(hip_fail(e, "hipHostMalloc"));
     for (int i = 0; i < 2; ++i) {
       if ((e = hipEventCreateWithFlags(&ctx->ev_copied[i], hipEventDisableTiming)) != hipSuccess)
         return cleanup(hip_fail(e, "hipEventCreate"));
@@ -629,6 +639,68 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
     }
     return run_items(ctx, f32_source(recording), items, tiles, out_dtype, out, static_cast<hipStream_t>(stream),
                      target_frames);
+  });
+}
+
+int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks,
+                               int32_t n, int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream) {
+  // sfe_extract_chunks with the item table and the raw log-mel in this
+  // device's static scratch: no device or host allocation on any path that
+  // succeeds (the item table is built in the context's pinned buffer, which
+  // sfe_create reserved for kNoAllocMaxItems items).
+  return guarded([&]() -> int {
+    if (n <= 0 || !tasks || !recording || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
+    if (n > sfe::kNoAllocMaxItems)
+      return fail(SFE_INVALID_ARG, "sfe_extract_chunks_noalloc takes at most " + std::to_string(sfe::kNoAllocMaxItems) +
+                                       " tasks");
+    int rc = check_dtype(out_dtype);
+    if (rc) return rc;
+    int64_t tiles = 0, fo = 0;
+    for (int32_t i = 0; i < n; ++i) {
+      const sfe_chunk& t = tasks[i];
+      if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
+        return fail(SFE_INVALID_ARG, "task " + std::to_string(i) + " lies outside the recording");
+      const int64_t L = t.audio_end - t.audio_start;
+      if (L == 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty (item " + std::to_string(i) + ")");
+      tiles += sfe::tiles_for(L / sfe::kHop + 1);
+    }
+    const size_t raw_bytes = (size_t)tiles * sfe::kRawTile * sizeof(float);
+    if (raw_bytes > sfe::kNoAllocRawBytes)
+      return fail(SFE_INVALID_ARG, "sfe_extract_chunks_noalloc: the tasks need " + std::to_string(raw_bytes) +
+                                       " bytes of scratch, more than its " + std::to_string(sfe::kNoAllocRawBytes));
+    if ((rc = check_ctx(ctx))) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (!ctx->noalloc || ctx->h_meta.cap < (size_t)n * sizeof(Item))
+      return fail(SFE_HIP_ERROR, "context has no static scratch");
+    // The pinned table is free once its previous upload has finished.
+    SFE_HIP(ctx->h_meta.wait());
+    Item* items = static_cast<Item*>(ctx->h_meta.ptr);
+    tiles = 0;
+    frame_offsets[0] = 0;
+    for (int32_t i = 0; i < n; ++i) {
+      Item& it = items[i];
+      it.start = tasks[i].audio_start;
+      it.len = tasks[i].audio_end - tasks[i].audio_start;
+      it.T = (int32_t)(it.len / sfe::kHop + 1);
+      it.out_off = (int64_t)sfe::kRawTile * tiles;
+      it.dst_off = (int64_t)sfe::kMel * fo;
+      it.tile_off = (int32_t)tiles;
+      fo += it.T;
+      tiles += sfe::tiles_for(it.T);
+      frame_offsets[i + 1] = fo;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(s, ctx->ev_last, 0));
+    Item* d_items = reinterpret_cast<Item*>(ctx->noalloc);
+    float* raw = reinterpret_cast<float*>(ctx->noalloc + sfe::kNoAllocItemBytes);
+    SFE_HIP(hipMemcpyAsync(d_items, items, (size_t)n * sizeof(Item), hipMemcpyHostToDevice, s));
+    SFE_HIP(hipEventRecord(ctx->h_meta.ev, s));
+    ctx->h_meta.pending = true;
+    rc = launch_pair(ctx, f32_source(recording), items, d_items, n, raw, out, out_dtype, 0, s, kBoth, false);
+    if (rc) return rc;
+    SFE_HIP(hipEventRecord(ctx->ev_last, s));
+    ctx->has_last = true;
+    return SFE_OK;
   });
 }
 

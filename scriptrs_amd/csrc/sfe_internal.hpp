@@ -95,6 +95,15 @@ constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: o
 hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max_T, int pad_to, void* out,
                        bool out_bf16, hipStream_t stream);
 
+// Static scratch of the allocation-free entry point (sfe_noalloc.hip): an
+// item table of up to kNoAllocMaxItems items, then kNoAllocRawBytes of raw
+// log-mel (kNoAllocRawBytes / (kRawTile * 4) 16-frame tiles).
+constexpr int kNoAllocMaxItems = 4096;
+constexpr size_t kNoAllocItemBytes = ((size_t)kNoAllocMaxItems * sizeof(Item) + 255) / 256 * 256;
+constexpr size_t kNoAllocRawBytes = (size_t)64 << 20;
+// Device address of this device's static scratch (looked up once per device).
+hipError_t noalloc_scratch(int device, void** out);
+
 // Silero VAD model inputs (sfe_vad.hip): [64 context | 512 window] f32 per
 // 512-sample window (src/long_form/vad.rs:62-99, src/constants.rs).
 constexpr int kVadWin = 512;

@@ -238,6 +238,25 @@ class ParakeetFeatureExtractor:
         _check(rc)
         return out, fo
 
+    def extract_chunks_noalloc(self, recording, tasks, dtype: str = "f32", stream=None, out=None):
+        """``extract_chunks`` through the allocation-free entry point: the
+        library keeps its item table and raw log-mel in a static per-GPU
+        array (at most 4096 tasks and 64 MiB of raw log-mel per call) and
+        allocates nothing.  Calls that overlap on one GPU race on that array.
+        ``out`` should be preallocated by callers that cannot allocate."""
+        import torch
+        _check_samples(recording, torch.float32)
+        tt = _tasks_array(tasks, self.config.hop_length)
+        fo = tt.frame_offsets.copy()
+        if out is None:
+            out = torch.empty(int(fo[-1]) * self.config.feature_size, dtype=_torch_dtype(dtype), device=recording.device)
+        _check_out(out, dtype, int(fo[-1]) * self.config.feature_size)
+        rc = _lib.lib().sfe_extract_chunks_noalloc(self._handle(), _dev_ptr(recording), recording.numel(), tt.ptr,
+                                                   tt.n, _dtype_code(dtype), _dev_ptr(out), _ip(fo),
+                                                   _stream_handle(stream))
+        _check(rc)
+        return out, fo
+
     def extract_chunks_pcm(self, recording, tasks, bits_per_sample: int | None = None, dtype: str = "f32",
                            stream=None, out=None):
         """``extract_chunks`` over a device recording of integer PCM (torch.int16

@@ -113,6 +113,25 @@ def test_batched_entry_points_validate_buffers_before_the_c_call():
     with pytest.raises(InvalidModelOutput, match="elements"):
         ext.extract_chunks_encoder_input(_FakeDeviceTensor(1600, f32), tasks, target_frames=1501,
                                          out=_FakeDeviceTensor(128 * 1500, f32))
+    with pytest.raises(InvalidModelOutput, match="elements"):
+        ext.extract_chunks_noalloc(_FakeDeviceTensor(1600, f32), tasks, out=_FakeDeviceTensor(5, f32))
     with pytest.raises(InvalidModelOutput, match="device tensor"):
         ext.extract_chunks(torch.zeros(1600), tasks, out=good)
     assert not ext._ctx  # nothing above reached the GPU
+
+
+def test_noalloc_limits_checked_before_any_device_work():
+    # more tasks than the static item table holds: rejected before the context is touched
+    tt = TaskTable(np.array([[i, i + 160, i, 0] for i in range(4097)], np.int64))
+    fo = np.zeros(tt.n + 1, np.int64)
+    rc = _lib.lib().sfe_extract_chunks_noalloc(None, ctypes.c_void_p(16), 10_000, tt.ptr, tt.n, 0,
+                                               ctypes.c_void_p(16), fo.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                               None)
+    assert rc == _lib.SFE_INVALID_ARG and "4096" in _lib.last_error()
+    # more raw scratch than the 64 MiB array: 30 min of audio in 15 s chunks
+    tt = TaskTable(build_fast_execution_plan(28_800_000))
+    fo = np.zeros(tt.n + 1, np.int64)
+    rc = _lib.lib().sfe_extract_chunks_noalloc(None, ctypes.c_void_p(16), 28_800_000, tt.ptr, tt.n, 0,
+                                               ctypes.c_void_p(16), fo.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                               None)
+    assert rc == _lib.SFE_INVALID_ARG and "scratch" in _lib.last_error()

@@ -19,7 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
 def test_host_logic_under_asan_ubsan(tmp_path):
-    for o in ("sfe_kernels.o", "sfe_vad.o"):
+    kobjs = ("sfe_kernels.o", "sfe_vad.o", "sfe_noalloc.o")
+    for o in kobjs:
         if not os.path.exists(os.path.join(OBJ, o)):
             pytest.skip("kernel objects not built (run build() first)")
     flags = ["-O1", "-g", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
@@ -38,7 +39,7 @@ def test_host_logic_under_asan_ubsan(tmp_path):
                    check=True, stderr=subprocess.DEVNULL)
     exe = str(tmp_path / "drv")
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-fsanitize=address,undefined", drv, *objs,
-                    os.path.join(OBJ, "sfe_kernels.o"), os.path.join(OBJ, "sfe_vad.o"), "-o", exe], check=True)
+                    *(os.path.join(OBJ, o) for o in kobjs), "-o", exe], check=True)
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0", UBSAN_OPTIONS="halt_on_error=1")
     r = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
