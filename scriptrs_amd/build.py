@@ -7,8 +7,10 @@ built ``.so`` travels with the source tree.
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -37,6 +39,40 @@ SOURCES = [
 ]
 
 
+# Kernel sources whose generated assembly is checked for MFMAs with a
+# destination overlapping their own A or B operand.  The register allocator
+# allows that overlap (it treats the operands as read at issue), but
+# v_mfma_f32_4x4x1_16b_f32 reads its A operand for some blocks after the
+# destination has been written, which gave wrong filters.
+MFMA_CHECKED = ("sfe_kernels.hip",)
+_MFMA_RE = re.compile(r"\bv_mfma\w*\s+v\[(\d+):(\d+)\],\s*v(\d+),\s*v(\d+)")
+
+
+def mfma_operand_overlaps(asm: str) -> list[str]:
+    """Lines of ``asm`` where an MFMA's VGPR destination range contains its
+    A or B operand register."""
+    bad = []
+    for line in asm.splitlines():
+        m = _MFMA_RE.search(line)
+        if m:
+            d0, d1, a, b = map(int, m.groups())
+            if d0 <= a <= d1 or d0 <= b <= d1:
+                bad.append(line.strip())
+    return bad
+
+
+def check_mfma(src: str, extra: list[str], verbose: bool = False) -> None:
+    with tempfile.TemporaryDirectory() as tmp:
+        out = os.path.join(tmp, "k.s")
+        cmd = [HIPCC, *COMMON, *extra, "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", out]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True, stderr=subprocess.DEVNULL)
+        bad = mfma_operand_overlaps(open(out).read())
+    if bad:
+        raise RuntimeError(f"{src}: MFMA destination overlaps its own A/B operand:\n  " + "\n  ".join(bad))
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     objs = []
@@ -47,6 +83,8 @@ def build(verbose: bool = False) -> str:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
         objs.append(obj)
+        if src in MFMA_CHECKED:
+            check_mfma(src, extra, verbose)
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:

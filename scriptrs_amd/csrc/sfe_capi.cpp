@@ -205,7 +205,7 @@ namespace {
 int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vector<Item>* items,
                 int64_t* frame_offsets, int64_t* total_tiles) {
   items->resize(n);
-  int64_t fo = 0, tiles = 0;
+  int64_t fo = 0, tiles = 0, units = 0;
   if (frame_offsets) frame_offsets[0] = 0;
   for (int32_t i = 0; i < n; ++i) {
     if (lens[i] <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty (item " + std::to_string(i) + ")");
@@ -217,12 +217,13 @@ int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vect
     it.out_off = (int64_t)sfe::kRawTile * tiles;  // raw scratch: whole 16-frame tiles per item
     it.dst_off = (int64_t)sfe::kMel * fo;
     it.T = (int32_t)T;
-    it.tile_off = (int32_t)tiles;
+    it.unit_off = (int32_t)units;
     fo += T;
     tiles += sfe::tiles_for(T);
+    units += sfe::units_for(T);
     if (frame_offsets) frame_offsets[i + 1] = fo;
+    if (units > INT32_MAX) return fail(SFE_INVALID_ARG, "batch too large for one launch");
   }
-  if (tiles > INT32_MAX) return fail(SFE_INVALID_ARG, "batch too large for one launch");
   *total_tiles = tiles;
   return SFE_OK;
 }
@@ -237,7 +238,7 @@ hipEvent_t timing_event(sfe_ctx* ctx) {
 }
 
 // Log-mel then normalisation over host items[0, n) (device copy d_items,
-// tile_off relative to the launch), asynchronously on `stream`.  With timing
+// unit_off relative to the launch), asynchronously on `stream`.  With timing
 // on, every kernel is bracketed by events (read by sfe_get_timing).  stages
 // selects the kernels: kLogmel, kNorm or both.
 //
@@ -252,8 +253,8 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* 
                 void* out, int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth,
                 bool allow_timing = true) {
   if (n <= 0) return SFE_OK;
-  const int u0 = items[0].tile_off;
-  const int u1 = items[n - 1].tile_off + (int)sfe::tiles_for(items[n - 1].T);
+  const int u0 = items[0].unit_off;
+  const int u1 = items[n - 1].unit_off + (int)sfe::units_for(items[n - 1].T);
   int max_T = 0;
   for (int i = 0; i < n; ++i) max_T = std::max(max_T, (int)items[i].T);
   hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -676,6 +677,7 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     SFE_HIP(ctx->h_meta.wait());
     Item* items = static_cast<Item*>(ctx->h_meta.ptr);
     tiles = 0;
+    int64_t units = 0;
     frame_offsets[0] = 0;
     for (int32_t i = 0; i < n; ++i) {
       Item& it = items[i];
@@ -684,9 +686,10 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
       it.T = (int32_t)(it.len / sfe::kHop + 1);
       it.out_off = (int64_t)sfe::kRawTile * tiles;
       it.dst_off = (int64_t)sfe::kMel * fo;
-      it.tile_off = (int32_t)tiles;
+      it.unit_off = (int32_t)units;
       fo += it.T;
       tiles += sfe::tiles_for(it.T);
+      units += sfe::units_for(it.T);
       frame_offsets[i + 1] = fo;
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -773,7 +776,7 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     struct Group {
       int32_t first, count;
       int64_t wstart, wend;
-      int32_t tiles, max_T;
+      int32_t units, max_T;
     };
     std::vector<Group> groups;
     for (int32_t i = 0; i < n;) {
@@ -821,11 +824,11 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
         const int32_t t0 = t;
         for (int32_t i = g.first; i < g.first + g.count; ++i) {
           items[i].start += base;
-          items[i].tile_off = t;
-          t += (int32_t)sfe::tiles_for(items[i].T);
+          items[i].unit_off = t;
+          t += (int32_t)sfe::units_for(items[i].T);
           g.max_T = std::max(g.max_T, (int)items[i].T);
         }
-        g.tiles = t - t0;
+        g.units = t - t0;
       }
     }
     const size_t mbytes = items.size() * sizeof(Item);

@@ -14,42 +14,35 @@ constexpr int kMel = 128;
 constexpr int kBins = kNfft / 2 + 1;  // 257
 constexpr int kPad = kNfft / 2;       // 256 zeros each side (src/frontend.rs:124-125)
 
-// Mel contraction schedule for v_mfma_f32_16x16x4_f32.  The 128 filters form
-// 8 blocks of 16; block b is contracted over kBlockSteps[b] steps of 4 bins
-// starting at a bin taken from the device table (so other sample rates work
-// when their filters fit the same step counts).  The step counts are those
-// of the 16 kHz Slaney filterbank.  Blocks are assigned to the 4 waves of a
-// workgroup at compile time so each wave's MFMA chains have static control
-// flow; the busiest wave runs 22 steps.
-constexpr int kWaves = 4;
-constexpr int kBlocks = kMel / 16;
-constexpr int kBlockSteps[kBlocks] = {4, 4, 4, 5, 8, 11, 15, 22};
-constexpr int kWaveBlocks[kWaves][3] = {{7, -1, -1}, {6, -1, -1}, {5, 3, 0}, {4, 2, 1}};
-constexpr int wave_steps(int w) {
-  int n = 0;
-  for (int i = 0; i < 3; ++i)
-    if (kWaveBlocks[w][i] >= 0) n += kBlockSteps[kWaveBlocks[w][i]];
-  return n;
-}
-constexpr int kMaxSteps = 22;  // per wave
-static_assert(wave_steps(0) <= kMaxSteps && wave_steps(1) <= kMaxSteps && wave_steps(2) <= kMaxSteps &&
-                  wave_steps(3) <= kMaxSteps,
-              "schedule exceeds the per-wave step budget");
+// Mel contraction schedule for v_mfma_f32_4x4x1_16b_f32.  One wave
+// contracts the power spectra of its own 4 frames: an MFMA is 16 blocks of
+// [4 filters x 1 bin] . [1 bin x 4 frames].  Chain 0 holds the blocks of
+// filters 0..63 (block j: filters 4j..4j+3), chain 1 those of filters
+// 64..127.  Block j of chain c runs kChainSteps[c] consecutive bins from its
+// own first bin (a multiple of 4, from the device table), so the dense
+// 128x257 product is never formed.  The step counts fit the 16 kHz Slaney
+// filterbank (widest block of chain 0: 7 bins, of chain 1: 32).
+constexpr int kChains = 2;
+constexpr int kChainSteps[kChains] = {8, 32};
+constexpr int kMelSteps = 40;       // both chains
+constexpr int kMelVec = kMelSteps / 4;  // float4 A operands per lane
+static_assert(kChainSteps[0] + kChainSteps[1] == kMelSteps && kChainSteps[0] % 4 == 0 && kChainSteps[1] % 4 == 0,
+              "chains are whole float4 steps");
 
 // One featurized item: a clip or a long-form chunk task.  samples[start,
 // start+len) is featurized into out[dst_off + m*S + t] (S = T, or the
 // padded row length of the encoder-input layout).  The raw log-mel (log2;
 // times ln 2 is the log-mel) goes to scratch in tiles of 16 frames: tile
 // t / 16 of the item at raw[out_off + 2048 * (t / 16)], holding 8 slabs of
-// 16 features, each [16 frames][16 features] (the slab order inside the tile
-// is the log-mel kernel's kSlabPos).
+// 16 features, each [16 frames][16 features], slab s holding features
+// 16s..16s+15.
 struct Item {
   int64_t start;
   int64_t len;
   int64_t out_off;   // raw (scratch) element offset: kRawTile * (tiles of the items before it)
   int64_t dst_off;   // output element offset: out_off when packed, i * feature_size * pad_to when padded
   int32_t T;         // len / hop + 1
-  int32_t tile_off;  // first 16-frame unit of this item, relative to the launch
+  int32_t unit_off;  // first unit (4-frame quad) of this item, relative to the launch
 };
 
 // Constant tables, uploaded once per context.
@@ -57,11 +50,12 @@ struct DevTables {
   float window[kNfft];       // hann_window(400), zero past 400
   float2 tw256[256];         // [l * 16 + k1] = e^{-2 pi i l k1 / 256}, l, k1 < 16
   float2 tw512[256];         // e^{-2 pi i k / 512}, k < 256
-  int32_t block_k0[kBlocks];               // first bin of each block (multiple of 4)
-  // A operand of each step of wave w, in the wave's block order, in lane
-  // order: lane L holds W[16 b + L % 16][k0_b + 4 s + L / 16] * 0.25 (the FFT
-  // stage yields 4|X|^2)
-  float a[kWaves][kMaxSteps][64];
+  // A operands of the mel MFMAs: [v][lane] holds steps 4v..4v+3 (v < 2:
+  // chain 0, else chain 1, steps 4(v-2)..) of lane L = 4j + m: filter
+  // 64c + 4j + m at bin k0[c][j] + step, times 0.25 (the FFT stage yields
+  // 4|X|^2).
+  float4 mel_a[kMelVec][64];
+  int32_t k0[kChains][16];  // first bin of each block (multiple of 4)
 };
 
 // Host table builders (sfe_tables.cpp).
@@ -71,9 +65,11 @@ void mel_filterbank(int n_fft, int n_mels, int sample_rate, float* out);
 bool build_dev_tables(int sample_rate, DevTables* t);
 
 // Kernel launchers (sfe_kernels.hip).  All asynchronous on `stream`.
-constexpr int kTile = 16;  // frames per unit of work (one pass) of the log-mel kernel
+constexpr int kTile = 16;  // frames per raw tile
 constexpr int kRawTile = kTile * 128;  // raw scratch floats per tile of 16 frames
+constexpr int kQuad = 4;   // frames per unit of work (one wave pass) of the log-mel kernel
 int64_t tiles_for(int64_t T);
+int64_t units_for(int64_t T);  // quads of an item: ceil(T / 4)
 // grid_cap: workgroups resident on the device at once (the kernel loops
 // over tiles, so launching more than that only adds scheduling overhead).
 // Input sample formats: f32, or integer PCM (16-bit or 32-bit containers)
@@ -81,11 +77,11 @@ int64_t tiles_for(int64_t T);
 constexpr int kPcmF32 = 0;
 constexpr int kPcmI16 = 1;
 constexpr int kPcmI32 = 2;
-// Units [unit0, unit0 + n_units) in the numbering of items[].tile_off.
+// Units [unit0, unit0 + n_units) in the numbering of items[].unit_off.
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
                          int n_units, const DevTables* tables, float preemph, float* raw_out, int grid_cap,
                          hipStream_t stream);
-constexpr int kLogmelWavesPerSimd = 2;
+constexpr int kLogmelWavesPerSimd = 3;
 constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
 // Normalises raw (f32 log2 values in 16-frame tiles, see Item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias

@@ -30,7 +30,8 @@
 namespace sfe {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kWaves = 4;               // log-mel workgroup: independent waves
+constexpr int kThreads = 64 * kWaves;
 constexpr int kXStride = 17;                         // transpose row stride (complex)
 constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
 constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
@@ -120,23 +121,22 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Work of one workgroup: a contiguous range of units; a unit is one pass of
-// 16 consecutive frames of one item.  In a pass each of the 4 waves
-// transforms 4 consecutive frames (16 lanes per frame) and writes their
-// power spectra to the shared P buffer; after one workgroup barrier every
-// wave contracts all 16 frames with its share of the mel filter blocks on
-// the matrix cores.  P is double-buffered, so a pass needs a single barrier.
-constexpr int kPassFrames = 16;
-static_assert(kTile == kPassFrames, "a unit of work is one 16-frame pass");
+// Work of one wave: a contiguous range of units; a unit (a quad) is 4
+// consecutive frames of one item.  Waves are independent: each owns an LDS
+// region in which its quad's samples, FFT transpose and power spectra live
+// in turn, and contracts its own 4 frames with all 128 filters on the matrix
+// cores (v_mfma_f32_4x4x1_16b_f32).  The only workgroup barrier is the one
+// after the A operands of those MFMAs are staged in LDS at kernel start.
 constexpr int kSpan = 3 * kHop + kWin;  // samples under 4 consecutive frames (880)
-constexpr int kWaveBuf = 4 * kSlot * 2; // floats: 4 transpose slots; also holds the 880-sample span
-constexpr int kPStride = 258;           // floats per P row (258 = 2 mod 32: conflict-free B reads)
+constexpr int kWaveBuf = 4 * kSlot * 2; // floats: 4 transpose slots; also holds the span and the power spectra
+constexpr int kPStride = 276;           // floats per power-spectrum row (frame)
 static_assert(kSpan <= kWaveBuf, "span must fit the wave buffer");
+static_assert(4 * kPStride <= kWaveBuf && kPStride >= kBins && kPStride % 4 == 0, "power rows fit the wave buffer");
 constexpr int kSpanVec = (kSpan + 255) / 256;  // 16-byte loads per lane (4)
 static_assert(kSpan % 4 == 0, "span is whole float4s");
 
-// The 880 samples under one wave's 4 frames of a unit: span sample j is
-// item sample s0 + j, valid for j in [jlo, jhi).
+// The 880 samples under one wave's quad: span sample j is item sample
+// s0 + j, valid for j in [jlo, jhi).
 template <typename S>
 struct Span {
   const S* xb;
@@ -146,8 +146,8 @@ struct Span {
 };
 
 template <typename S>
-__device__ __forceinline__ Span<S> make_span(const Item& it, const S* samples, int u, int w) {
-  const int fw = (u - it.tile_off) * kPassFrames + 4 * w;
+__device__ __forceinline__ Span<S> make_span(const Item& it, const S* samples, int u) {
+  const int fw = (u - it.unit_off) * kQuad;
   Span<S> sp;
   sp.s0 = (int64_t)fw * kHop - kPad;
   sp.jlo = sp.s0 < 0 ? (int)(-sp.s0) : 0;
@@ -189,103 +189,35 @@ __device__ __forceinline__ float4 ln2_scale(float4 v) {
   return make_float4(v.x * kLn2, v.y * kLn2, v.z * kLn2, v.w * kLn2);
 }
 
-// Independent accumulator chains per block: a long block's steps alternate
-// between chains so consecutive MFMAs do not wait on each other.
-template <int B>
-constexpr int block_chains() {
-  return kBlockSteps[B] >= 16 ? 3 : (kBlockSteps[B] >= 8 ? 2 : 1);
+// Raw log-mel is written in tiles of 16 frames: 8 slabs of 16 features, each
+// slab [16 frames][16 features] (1 KB), slab s holding features 16s..16s+15.
+// After a quad's MFMAs, lane 4j + n holds filters 4j..4j+3 (chain 0) and
+// 64 + 4j..+3 (chain 1) of frame n: two aligned 16-byte stores per lane, and
+// one store instruction writes 4 slabs x 256 contiguous bytes.  The
+// normalisation kernel, which works per (item, slab), reads 1 KB contiguous
+// per load instruction.
+__device__ __forceinline__ float4 log4(const f32x4& v) {
+  return make_float4(guarded_log2(v[0]), guarded_log2(v[1]), guarded_log2(v[2]), guarded_log2(v[3]));
 }
 
-// One wave's mel results for one pass: D[j] holds block kWaveBlocks[W][j];
-// lane (n, kk) holds filters 16 b + 4 kk + r of frame n.
-struct MelAcc {
-  f32x4 d[3];
-};
-
-// MFMA chains of all of a wave's filter blocks for one pass.  Every B
-// operand is read from LDS before the first MFMA is issued (one LDS wait),
-// and the chains of a long block alternate between accumulators so
-// consecutive MFMAs do not wait on each other.  The results are consumed a
-// pass later (mel_store), so the MFMA latency hides behind the next FFT.
-template <int W>
-__device__ __forceinline__ void mel_mfma(const float (&av)[kMaxSteps], const int (&k0b)[kBlocks], const float* PB,
-                                         MelAcc& acc) {
-  constexpr int b[3] = {kWaveBlocks[W][0], kWaveBlocks[W][1], kWaveBlocks[W][2]};
-  constexpr int S[3] = {kBlockSteps[b[0]], b[1] >= 0 ? kBlockSteps[b[1] < 0 ? 0 : b[1]] : 0,
-                        b[2] >= 0 ? kBlockSteps[b[2] < 0 ? 0 : b[2]] : 0};
-  constexpr int NS = S[0] + S[1] + S[2];
-  static_assert(NS <= kMaxSteps, "wave step budget");
-  float bv[NS];
-#pragma unroll
-  for (int j = 0, s0 = 0; j < 3; s0 += S[j], ++j)
-#pragma unroll
-    for (int s = 0; s < S[j]; ++s) bv[s0 + s] = PB[k0b[b[j] < 0 ? 0 : b[j]] + 4 * s];
-  __builtin_amdgcn_sched_barrier(0);
-  // Two accumulators per block (three for the longest), interleaved.
-  f32x4 c[3][3];
-#pragma unroll
-  for (int j = 0; j < 3; ++j)
-#pragma unroll
-    for (int q = 0; q < 3; ++q) c[j][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int j = 0, s0 = 0; j < 3; s0 += S[j], ++j) {
-#pragma unroll
-    for (int s = 0; s < S[j]; ++s) {
-      const int q = S[j] >= 16 ? s % 3 : (S[j] >= 8 ? s % 2 : 0);
-      c[j][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s0 + s], bv[s0 + s], c[j][q], 0, 0, 0);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    if (S[j] >= 16) acc.d[j] = c[j][0] + c[j][1] + c[j][2];
-    else if (S[j] >= 8) acc.d[j] = c[j][0] + c[j][1];
-    else acc.d[j] = c[j][0];
-  }
-}
-
-// Raw log-mel is written in tiles of 16 frames (one pass): 8 slabs of 16
-// features, each slab [16 frames][16 features] (1 KB).  Lane (n, kk) holds
-// filters 16 b + 4 kk .. + 3 of frame n: one aligned 16-byte store, and one
-// store instruction writes a whole contiguous slab.  The normalisation
-// kernel, which works per (item, slab), then reads 1 KB contiguous per load
-// instruction.  (Frame-major [T][128] rows made it read 64-byte pieces:
-// 0.095 ms against 0.079 ms for the 1 h workload; this layout costs log-mel
-// 2%.)  Slabs sit in the tile in the order of the waves' filter blocks
-// (kWaveBlocks: 7 | 6 | 5 3 0 | 4 2 1), so each wave's stores are
-// adjacent and share one base address.
-constexpr int kSlabPos[kBlocks] = {4, 7, 6, 3, 5, 2, 1, 0};
-__device__ __forceinline__ void store_block(const f32x4& v, int b, float* frame_row, int kk) {
-  *reinterpret_cast<float4*>(frame_row + 256 * kSlabPos[b] + 4 * kk) =
-      make_float4(guarded_log2(v[0]), guarded_log2(v[1]), guarded_log2(v[2]), guarded_log2(v[3]));
-}
-
-template <int W>
-__device__ __forceinline__ void mel_store(const MelAcc& acc, float* frame_row, int kk) {
-  constexpr int b0 = kWaveBlocks[W][0], b1 = kWaveBlocks[W][1], b2 = kWaveBlocks[W][2];
-  store_block(acc.d[0], b0, frame_row, kk);
-  if constexpr (b1 >= 0) store_block(acc.d[1], b1, frame_row, kk);
-  if constexpr (b2 >= 0) store_block(acc.d[2], b2, frame_row, kk);
-}
-
-// Log and store of the previous pass's mel results (pending when valid).
-__device__ __forceinline__ void store_pending(int w, const MelAcc& acc, float* frame_row, bool valid, int kk) {
-  if (!valid) return;
-  switch (w) {
-    case 0: mel_store<0>(acc, frame_row, kk); break;
-    case 1: mel_store<1>(acc, frame_row, kk); break;
-    case 2: mel_store<2>(acc, frame_row, kk); break;
-    default: mel_store<3>(acc, frame_row, kk); break;
-  }
+// Keeps a float4 of MFMA A operands and one of B operands allocated up to
+// this point (an empty asm that reads them), placed after their MFMAs with a
+// scheduling barrier between.  Otherwise the register allocator may give an
+// MFMA a destination overlapping one of its own operands (their last use),
+// and v_mfma_f32_4x4x1_16b_f32 reads its A operand for some blocks after the
+// destination has been written: a first version of this kernel got 48 of the
+// 128 filters wrong that way.  The build rejects any MFMA whose destination
+// overlaps its A or B operand in the generated assembly.
+__device__ __forceinline__ void mfma_keep(const float4& a, const float4& b) {
+  asm volatile("" ::"v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(b.x), "v"(b.y), "v"(b.z), "v"(b.w));
 }
 
 template <typename S>
-__global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kernel(const S* __restrict__ samples,
-                                                              const Item* __restrict__ items, int n_items,
-                                                              int unit0, int n_units,
-                                                              const DevTables* __restrict__ tb, float coef,
-                                                              Decode dc, float* __restrict__ out) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kLogmelWavesPerSimd, kLogmelWavesPerSimd)))
+void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ items, int n_items, int unit0,
+                       int n_units, const DevTables* __restrict__ tb, float coef, Decode dc, float* __restrict__ out) {
   __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
-  __shared__ __align__(16) float pbuf[2][kPassFrames][kPStride];
+  __shared__ __align__(16) float4 mel_a[kMelVec][64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -294,9 +226,12 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
   const int l = lane & 15;
   const int partner = (16 - l) & 15;
 
+  // A operands of the mel MFMAs, shared by the workgroup's waves.
+  for (int i = tid; i < kMelVec * 64; i += kThreads) mel_a[i / 64][i % 64] = tb->mel_a[i / 64][i % 64];
+  __syncthreads();
+
   // Per-lane constants: window taps of this lane's FFT inputs, inter-stage
-  // twiddles e^{-2 pi i l k1/256}, split twiddles e^{-2 pi i k/512}, and the
-  // A operands (filter weights) of this wave's MFMA steps.
+  // twiddles e^{-2 pi i l k1/256}, split twiddles e^{-2 pi i k/512}.
   cf wv[13];
 #pragma unroll
   for (int m2 = 0; m2 < 13; ++m2) {
@@ -312,32 +247,35 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
     float2 tw = tb->tw256[l * 16 + k1];
     t256[k1] = {tw.x, tw.y};
   }
-  cf t512[9];
+  // k2 = 8 is not held: e^{-2 pi i (k + 128)/512} = -i e^{-2 pi i k/512}
+  // follows from k2 = 0 by swapping and negating parts.
+  cf t512[8];
 #pragma unroll
-  for (int k2 = 0; k2 < 9; ++k2) {
+  for (int k2 = 0; k2 < 8; ++k2) {
     float2 tw = tb->tw512[l + 16 * k2];
     t512[k2] = {tw.x, tw.y};
   }
-  float av[kMaxSteps];
-#pragma unroll
-  for (int s = 0; s < kMaxSteps; ++s) av[s] = tb->a[w][s][lane];
-  int k0b[kBlocks];  // first bin of each filter block (uniform)
-#pragma unroll
-  for (int b = 0; b < kBlocks; ++b) k0b[b] = tb->block_k0[b];
 
   float* sb = wbuf[w];
   cf* X = reinterpret_cast<cf*>(sb) + g * kSlot;
-  const int n = lane & 15;        // MFMA: B column (frame) / D column
-  const int kk = lane >> 4;       // MFMA: B row (bin within the step) / D row group
+  // MFMA B operands: lane 4j + n reads frame n's power from the first bin of
+  // block j of each chain.
+  const int mj = lane >> 2, mn = lane & 3;
+  const float* pb0 = sb + mn * kPStride + tb->k0[0][mj];
+  const float* pb1 = sb + mn * kPStride + tb->k0[1][mj];
+  // Store offset of this lane's filters within a raw tile: frame row mn,
+  // slab mj / 4 (chain 0; chain 1 is 4 slabs on), 4 features at 4 (mj % 4).
+  const int so = 16 * mn + 256 * (mj >> 2) + 4 * (mj & 3);
 
-  // Persistent grid: each workgroup walks one contiguous range of units
-  // (16-frame passes of one item), so the per-lane constants above are
-  // loaded once per workgroup and neighbouring units (which share cache
-  // lines of the output rows and of the input) stay on one XCD's L2.
-  // Units of this launch are [unit0, unit0 + n_units) (items[].tile_off
+  // Persistent grid: each wave walks one contiguous range of units (quads
+  // of one item), so the per-lane constants above are loaded once per wave
+  // and neighbouring units, which share input lines, stay in one cache.
+  // Units of this launch are [unit0, unit0 + n_units) (items[].unit_off
   // counts in the same numbering).
-  const int u_begin = unit0 + (int)((int64_t)n_units * blockIdx.x / gridDim.x);
-  const int u_end = unit0 + (int)((int64_t)n_units * (blockIdx.x + 1) / gridDim.x);
+  const int64_t nw = (int64_t)gridDim.x * kWaves;
+  const int64_t gw = (int64_t)blockIdx.x * kWaves + w;
+  const int u_begin = unit0 + (int)((int64_t)n_units * gw / nw);
+  const int u_end = unit0 + (int)((int64_t)n_units * (gw + 1) / nw);
   if (u_begin >= u_end) return;
   // Item descriptors stay in scalar registers: it_c is the item of the unit
   // being prefetched, it_n the item after it, loaded one item ahead so an
@@ -347,7 +285,7 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
     int hi = n_items - 1;
     while (li < hi) {
       int mid = (li + hi + 1) >> 1;
-      if (items[mid].tile_off <= u_begin) li = mid;
+      if (items[mid].unit_off <= u_begin) li = mid;
       else hi = mid - 1;
     }
   }
@@ -355,14 +293,14 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
   Item it_n = items[li + 1 < n_items ? li + 1 : li];
   // The samples of unit u + 1 are loaded into registers while unit u is
   // transformed, so the global-load latency hides behind the FFT.
-  Span<S> sp_n = make_span(it_c, samples, u_begin, w);
+  Span<S> sp_n = make_span(it_c, samples, u_begin);
   typename Pcm<S>::V4 nv[kSpanVec] = {};
   S nxm1 = 0;
   prefetch_span(sp_n, lane, nv, nxm1);
 
-  MelAcc acc;
-  float* pend_row = out;
-  bool pend = false;  // acc holds a pass whose log-mel is not yet stored
+  f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+  // Raw offset (uniform) of the quad whose log-mel is held in acc0/acc1, or -1.
+  int64_t pend = -1;
 
   for (int u = u_begin; u < u_end; ++u) {
     const Item it = it_c;
@@ -373,11 +311,12 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
 #pragma unroll
     for (int h = 0; h < kSpanVec; ++h) cv[h] = Pcm<S>::dec4(nv[h], dc);
     const float cxm1 = Pcm<S>::dec(nxm1, dc);
-    float* o = out + it.out_off;
 
     // ---- 1. preemphasised, zero-padded samples of this wave's 4 frames
     // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
-    // src/frontend.rs:157 computes it), zero outside [0, L).
+    // src/frontend.rs:157 computes it), zero outside [0, L).  The previous
+    // quad's MFMA reads of this buffer were issued earlier, and LDS
+    // operations of a wave complete in order.
     if (sp.interior) {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -421,18 +360,22 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
         }
       }
     }
-    // The previous pass's log-mel goes out while the span's LDS writes land.
-    store_pending(w, acc, pend_row, pend, kk);
+    // The previous quad's log-mel goes out while the span's LDS writes land.
+    if (pend >= 0) {
+      float* o = out + pend;
+      *reinterpret_cast<float4*>(o + so) = log4(acc0);
+      *reinterpret_cast<float4*>(o + so + 4 * 256) = log4(acc1);
+    }
     // Then the next unit's samples are requested.  Vector memory operations
     // complete in issue order, so loading after the stores means the wait
-    // for these samples, a pass from now, never waits on fresh stores.
+    // for these samples, a quad from now, never waits on fresh stores.
     if (u + 1 < u_end) {
-      if (li + 1 < n_items && u + 1 >= it_n.tile_off) {
+      if (li + 1 < n_items && u + 1 >= it_n.unit_off) {
         ++li;
         it_c = it_n;
         it_n = items[li + 1 < n_items ? li + 1 : li];
       }
-      sp_n = make_span(it_c, samples, u + 1, w);
+      sp_n = make_span(it_c, samples, u + 1);
       prefetch_span(sp_n, lane, nv, nxm1);
     }
     wave_lds_sync();
@@ -473,20 +416,17 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
       const cf src = a[(15 - k2) & 15];
       sh[k2] = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
     }
-    // From here to the pass barrier the wave runs at raised priority: the
-    // workgroup's other waves wait for it at the barrier, so the SIMD's
-    // other wave (another workgroup's) yields to it.  Measured 1.8% faster
-    // on the 1 h workload; starting the raised priority earlier (at the
-    // window or transpose phases) was 5% slower.
-    __builtin_amdgcn_s_setprio(2);
-    float* P = pbuf[u & 1][4 * w + g];
+    // The power rows overwrite the transpose slots: every lane's reads of
+    // them above were issued first.
+    float* P = sb + g * kPStride;
 #pragma unroll
     for (int k2 = 0; k2 < 9; ++k2) {
       const cf A = a[k2];
       const cf B = (l == 0) ? a[(16 - k2) & 15] : sh[k2];
       cf e = {A.x + B.x, A.y - B.y};
       cf od = {A.y + B.y, B.x - A.x};
-      cf t = cmul(od, t512[k2]);
+      const cf tw = t512[k2 & 7];
+      cf t = cmul(od, k2 < 8 ? tw : cf{tw.y, -tw.x});
       cf xp = cadd(e, t), xm = csub(e, t);
       float pp = xp.x * xp.x + xp.y * xp.y;
       float pm = xm.x * xm.x + xm.y * xm.y;
@@ -498,23 +438,51 @@ __global__ __launch_bounds__(kThreads, kLogmelWavesPerSimd) void sfe_logmel_kern
         P[128] = pp;
       }
     }
-    __syncthreads();  // all 16 power spectra of this pass are in pbuf[u & 1]
-    __builtin_amdgcn_s_setprio(0);
+    wave_lds_sync();
 
-    // ---- 3. mel on the matrix cores: D[filter][frame] += W[filter][4 bins] . P[4 bins][frame]
-    const float* PB = &pbuf[u & 1][n][kk];
-    switch (w) {
-      case 0: mel_mfma<0>(av, k0b, PB, acc); break;
-      case 1: mel_mfma<1>(av, k0b, PB, acc); break;
-      case 2: mel_mfma<2>(av, k0b, PB, acc); break;
-      default: mel_mfma<3>(av, k0b, PB, acc); break;
+    // ---- 3. mel on the matrix cores: block j of chain c accumulates
+    // W[64c + 4j + m][k0 + s] . P[frame n][k0 + s] over its steps s, 4 steps
+    // (one float4 of A and of B operands) per group; the next group's
+    // operands are loaded while this group's MFMAs issue.
+    f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0;
+    float4 a1n = mel_a[kChainSteps[0] / 4][lane], b1n = *reinterpret_cast<const float4*>(pb1);
+    float4 a0n = mel_a[0][lane], b0n = *reinterpret_cast<const float4*>(pb0);
+#pragma unroll
+    for (int v = 0; v < kChainSteps[1] / 4; ++v) {
+      const float4 a1 = a1n, b1 = b1n, a0 = a0n, b0 = b0n;
+      if (v + 1 < kChainSteps[1] / 4) {
+        a1n = mel_a[kChainSteps[0] / 4 + v + 1][lane];
+        b1n = *reinterpret_cast<const float4*>(pb1 + 4 * (v + 1));
+      }
+      if (v + 1 < kChainSteps[0] / 4) {
+        a0n = mel_a[v + 1][lane];
+        b0n = *reinterpret_cast<const float4*>(pb0 + 4 * (v + 1));
+      }
+      c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.x, b1.x, c1, 0, 0, 0);
+      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.x, b0.x, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.y, b1.y, c1, 0, 0, 0);
+      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.y, b0.y, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.z, b1.z, c1, 0, 0, 0);
+      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.z, b0.z, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.w, b1.w, c1, 0, 0, 0);
+      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.w, b0.w, c0, 0, 0, 0);
+      // The group's operands stay allocated past its MFMAs (see mfma_keep).
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_keep(a1, b1);
+      if (v < kChainSteps[0] / 4) mfma_keep(a0, b0);
     }
-    // Every frame of the pass is stored: frames past the item's end land in
-    // its last tile's padding, which nothing reads (1% faster than masking).
-    pend = true;
-    pend_row = o + (int64_t)kRawTile * (u - it.tile_off) + 16 * n;  // this pass's tile, frame n's slab rows
+    acc0 = c0;
+    acc1 = c1;
+    // Every frame of the quad is stored: frames past the item's end land in
+    // its last tile's padding, which nothing reads.
+    const int q = u - it.unit_off;
+    pend = it.out_off + (int64_t)kRawTile * (q >> 2) + 64 * (q & 3);
   }
-  store_pending(w, acc, pend_row, pend, kk);
+  if (pend >= 0) {
+    float* o = out + pend;
+    *reinterpret_cast<float4*>(o + so) = log4(acc0);
+    *reinterpret_cast<float4*>(o + so + 4 * 256) = log4(acc1);
+  }
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
@@ -754,10 +722,10 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   const Item it = items[item];
   const int T = it.T;
   // Uniform bases with 32-bit lane offsets.  Raw tiles hold 16 frames, each
-  // slab 1 KB frame-major inside (kSlabPos): frame f of this slab sits at
+  // slab 1 KB frame-major inside: frame f of this slab sits at
   // xb + kRawTile * (f / 16) + 16 * (f % 16).
   static_assert(F == 16 && S::kGroup == 16, "one wave's load covers one tile of one slab");
-  const float* xb = raw + it.out_off + 256 * kSlabPos[slab / 16];
+  const float* xb = raw + it.out_off + 256 * (slab / 16);
   const int rs = pad_to > 0 ? pad_to : T;  // output row length
   O* ob = out + it.dst_off + (size_t)slab * rs;
   if (pad_to > 0) zero_tail<W, F>(ob, T, rs, lane, w);
@@ -907,12 +875,15 @@ __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const flo
 }  // namespace
 
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
+int64_t units_for(int64_t T) { return (T + kQuad - 1) / kQuad; }
 
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
                          int n_units, const DevTables* tables, float preemph, float* raw_out, int grid_cap,
                          hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
-  const int grid = n_units < grid_cap ? n_units : grid_cap;
+  // Each wave takes at least one unit; at most grid_cap workgroups are resident.
+  const int want = (n_units + kWaves - 1) / kWaves;
+  const int grid = want < grid_cap ? want : grid_cap;
   Decode dc{pcm_scale, 1.0f / pcm_scale, 1.0 / (double)pcm_scale};  // the host's divisions are correctly rounded
   const dim3 g(grid), b(kThreads);
   if (pcm == kPcmI16)

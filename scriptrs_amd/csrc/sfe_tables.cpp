@@ -74,31 +74,30 @@ bool build_dev_tables(int sample_rate, DevTables* t) {
   }
   std::vector<float> fb((size_t)kMel * kBins);
   mel_filterbank(kNfft, kMel, sample_rate, fb.data());
-  // 16-filter blocks: the first bin (multiple of 4) is chosen here; the
-  // block's nonzero bins must fit the compiled step count.
-  for (int b = 0; b < kBlocks; ++b) {
-    int lo = -1, hi = -1;
-    for (int m = 16 * b; m < 16 * b + 16; ++m)
-      for (int k = 0; k < kBins; ++k)
-        if (fb[(size_t)m * kBins + k] != 0.0f) {
-          if (lo < 0 || k < lo) lo = k;
-          if (k > hi) hi = k;
-        }
-    if (lo < 0) lo = hi = 0;
-    const int k0 = lo / 4 * 4;
-    if (hi >= k0 + 4 * kBlockSteps[b]) return false;  // filters too wide for this schedule
-    if (k0 + 4 * kBlockSteps[b] > kBins) return false;            // reads stay within the 257 bins
-    t->block_k0[b] = k0;
-  }
-  for (int w = 0; w < kWaves; ++w) {
-    int s = 0;
-    for (int i = 0; i < 3; ++i) {
-      const int b = kWaveBlocks[w][i];
-      if (b < 0) continue;
-      for (int j = 0; j < kBlockSteps[b]; ++j, ++s)
-        for (int L = 0; L < 64; ++L) {
-          int m = 16 * b + L % 16, k = t->block_k0[b] + 4 * j + L / 16;
-          t->a[w][s][L] = fb[(size_t)m * kBins + k] * 0.25f;
+  // 4-filter blocks: the first bin (a multiple of 4) is chosen here; the
+  // block's nonzero bins must fit its chain's step count, and every bin
+  // read must lie within the 257 bins the FFT stage writes.
+  for (int c = 0; c < kChains; ++c) {
+    const int S = kChainSteps[c];
+    for (int j = 0; j < 16; ++j) {
+      const int f0 = 64 * c + 4 * j;
+      int lo = -1, hi = -1;
+      for (int m = f0; m < f0 + 4; ++m)
+        for (int k = 0; k < kBins; ++k)
+          if (fb[(size_t)m * kBins + k] != 0.0f) {
+            if (lo < 0 || k < lo) lo = k;
+            if (k > hi) hi = k;
+          }
+      if (lo < 0) lo = hi = 0;
+      int k0 = lo / 4 * 4;
+      if (k0 + S > kBins) k0 = (kBins - S) / 4 * 4;
+      if (lo < k0 || hi >= k0 + S) return false;  // filters too wide for this schedule
+      t->k0[c][j] = k0;
+      for (int s = 0; s < S; ++s)
+        for (int m = 0; m < 4; ++m) {
+          const int v = (c == 0 ? 0 : kChainSteps[0] / 4) + s / 4;
+          float* a = reinterpret_cast<float*>(&t->mel_a[v][4 * j + m]);
+          a[s % 4] = fb[(size_t)(f0 + m) * kBins + k0 + s] * 0.25f;
         }
     }
   }

@@ -218,3 +218,13 @@ def test_pcm_argument_errors_before_device():
         rc = L.sfe_extract_chunks_pcm(None, ctypes.cast(buf, ctypes.c_void_p), fmt, bits, 1000, t, 1, 0,
                                       ctypes.cast(buf, ctypes.c_void_p), fo, None)
         assert rc == _lib.SFE_INVALID_ARG, (fmt, bits)
+
+
+def test_build_rejects_mfma_destination_overlapping_its_operands():
+    from scriptrs_amd.build import mfma_operand_overlaps
+    asm = ("\tv_mfma_f32_4x4x1_16b_f32 v[46:49], v49, v57, v[62:65]\n"   # dst holds its own A operand
+           "\tv_mfma_f32_4x4x1_16b_f32 v[50:53], v1, v51, v[50:53]\n"    # dst holds its own B operand
+           "\tv_mfma_f32_4x4x1_16b_f32 v[46:49], v50, v57, v[46:49]\n"   # in-place accumulate: fine
+           "\tv_mfma_f32_4x4x1_16b_f32 a[0:3], v2, v3, a[0:3]\n")        # AGPR accumulator: fine
+    bad = mfma_operand_overlaps(asm)
+    assert len(bad) == 2 and "v49" in bad[0] and "v51" in bad[1]
