@@ -84,6 +84,40 @@ def extract(audio: np.ndarray) -> np.ndarray:
     return normalize(logmel_raw(audio))
 
 
+# An element is near the noise floor when its float64 mel energy is at most
+# this fraction of its frame's energy (sum of |X_k|^2).  f32 FFT rounding is
+# of order u log2(N) ||frame|| per bin, so only such elements can move by
+# more than the 1e-4 / 1e-3 bar (observed: at most 1.6e-8 of the frame
+# energy on the speech-like workloads).
+NEAR_GUARD_RATIO = 1e-6
+# The envelope never widens an element by more than this (normalised units;
+# observed maximum 3.4e-3).
+ENV_CAP = 5e-3
+
+
+def _frames_f64(audio: np.ndarray):
+    x = np.asarray(audio, np.float64)
+    w = hann_window_f32().astype(np.float64)
+    y = np.empty_like(x)
+    y[0] = x[0]
+    y[1:] = x[1:] - np.float64(np.float32(0.97)) * x[:-1]
+    padded = np.concatenate([np.zeros(N_FFT // 2), y, np.zeros(N_FFT // 2)])
+    T = x.size // HOP + 1
+    idx = np.arange(T)[:, None] * HOP + np.arange(WIN)[None, :]
+    return padded[idx] * w[None, :]
+
+
+def near_guard(audio: np.ndarray) -> np.ndarray:
+    """[128, T] bool: elements whose float64 mel energy is at most
+    NEAR_GUARD_RATIO of their frame's energy (frames of zero energy are
+    exact in every implementation and are not near-guard)."""
+    frames = _frames_f64(audio)
+    P = np.abs(np.fft.rfft(frames, n=N_FFT, axis=1)) ** 2
+    mel = P @ slaney_mel_filterbank().T
+    E = P.sum(1, keepdims=True)
+    return ((mel <= NEAR_GUARD_RATIO * E) & (E > 0)).T
+
+
 def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
     """Per-element scale of the rounding noise any f32 FFT-based implementation
     of the front end carries, in normalised units, [128, T].
@@ -93,17 +127,12 @@ def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
     |X_k|^2 by about 2|X_k| dX + dX^2, the mel value by the filter-weighted
     sum of that, the log by dmel / (mel + 2^-24), and the normalised output
     by that divided by the row's std.  A floor of 4u*|raw| covers the f32 log
-    and elementwise rounding."""
-    x = np.asarray(audio, np.float64)
-    w = hann_window_f32().astype(np.float64)
+    and elementwise rounding.  The envelope is zero except on near-guard
+    elements (near_guard) and at most ENV_CAP: only those elements may be
+    widened past the flat bar."""
+    frames = _frames_f64(audio)
     fb = slaney_mel_filterbank()
-    y = np.empty_like(x)
-    y[0] = x[0]
-    y[1:] = x[1:] - np.float64(np.float32(0.97)) * x[:-1]
-    padded = np.concatenate([np.zeros(N_FFT // 2), y, np.zeros(N_FFT // 2)])
-    T = x.size // HOP + 1
-    idx = np.arange(T)[:, None] * HOP + np.arange(WIN)[None, :]
-    frames = padded[idx] * w[None, :]
+    T = frames.shape[0]
     X = np.abs(np.fft.rfft(frames, n=N_FFT, axis=1))
     u = 2.0 ** -24
     dX = u * np.log2(N_FFT) * np.sqrt((frames ** 2).sum(1, keepdims=True))
@@ -112,4 +141,7 @@ def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
     raw = np.log(mel + 2.0 ** -24)
     d_raw = (dP @ fb.T) / (mel + 2.0 ** -24) + 4 * u * np.abs(raw)
     std = raw.std(axis=0, ddof=1, keepdims=True) if T > 1 else np.ones((1, raw.shape[1]))
-    return (d_raw / std).T
+    E = (X ** 2).sum(1, keepdims=True)
+    near = (mel <= NEAR_GUARD_RATIO * E) & (E > 0)
+    env = np.where(near, np.minimum(d_raw / std, ENV_CAP), 0.0)
+    return env.T

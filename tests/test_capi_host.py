@@ -228,3 +228,91 @@ def test_build_rejects_mfma_destination_overlapping_its_operands():
            "\tv_mfma_f32_4x4x1_16b_f32 a[0:3], v2, v3, a[0:3]\n")        # AGPR accumulator: fine
     bad = mfma_operand_overlaps(asm)
     assert len(bad) == 2 and "v49" in bad[0] and "v51" in bad[1]
+
+
+def _closed_form_plan(n, chunk=238_080, stride=206_080, ctx=1280, hop=160):
+    """Count, sum of task lengths and sum of frame counts of the fast plan,
+    in closed form: task i covers [max(i*stride - ctx, 0), min(i*stride +
+    chunk, n)) and the plan ends with the first task that reaches n, so
+    count = ceil((n - chunk) / stride) + 1 (1 when n <= chunk).  Lengths:
+    the first task has no context; middle tasks are chunk + ctx; the last
+    runs to n (src/long_form/planner.rs:124-137, src/long_form.rs:566-582)."""
+    if n <= 0:
+        return 0, 0, 0
+    count = 1 if n <= chunk else -(-(n - chunk) // stride) + 1
+    lens = []
+    for i in range(count):
+        lo, hi = max(i * stride - ctx, 0), min(i * stride + chunk, n)
+        lens.append(hi - lo)
+    return count, sum(lens), sum(L // hop + 1 for L in lens)
+
+
+@pytest.mark.parametrize("n", [1, 238_080, 238_081, 444_160, 444_161, 1_000_003, 28_800_000, 57_600_000,
+                               460_800_000])
+def test_planner_matches_closed_form(n):
+    """The library's plan against the closed form above, without the
+    restated planner.  The constants follow from the reference's defaults:
+    chunk = (240000 - 1280 - 160) // 1280 * 1280 = 238080, overlap =
+    min(32000, 119040) // 1280 * 1280 = 32000, stride = 206080."""
+    assert (240_000 - 1280 - 160) // 1280 * 1280 == 238_080
+    assert min(2 * 16_000, 238_080 // 2) // 1280 * 1280 == 32_000 and 238_080 - 32_000 == 206_080
+    t = build_fast_execution_plan(n)
+    got = (len(t), sum(x.audio_end - x.audio_start for x in t), sum((x.audio_end - x.audio_start) // 160 + 1 for x in t))
+    assert got == _closed_form_plan(n)
+    if n == 57_600_000:
+        assert got == (280, 66_885_120, 418_312)
+    if n == 460_800_000:
+        assert got == (2236, 535_180_800, 3_347_116)
+    # every task starts on the stride grid and the last one ends at n
+    assert [x.global_sample_offset for x in t] == [i * 206_080 for i in range(len(t))]
+    assert t[-1].audio_end == n and all(x.context_samples == x.global_sample_offset - x.audio_start for x in t)
+
+
+def _markstein_f64(v32, scale, recip):
+    """Vectorised kernel decode for f32 inputs: q = RN32(v r); e = RN32(v -
+    scale q) (scale q is exact in f64 and v - scale q is exact by Sterbenz);
+    RN32(q + e r) with e r exact in f64.  The sum q + e r is rounded twice (f64
+    then f32), so values whose f64 sum lies within an f64 ulp of an f32
+    rounding midpoint are returned in `hard` for an exact check."""
+    q = (v32 * recip).astype(np.float32)
+    e = (v32.astype(np.float64) - np.float64(scale) * q.astype(np.float64)).astype(np.float32)
+    s64 = q.astype(np.float64) + e.astype(np.float64) * np.float64(recip)
+    out = s64.astype(np.float32)
+    # f32 midpoints around the result
+    up = np.nextafter(out, np.float32(np.inf)).astype(np.float64)
+    dn = np.nextafter(out, np.float32(-np.inf)).astype(np.float64)
+    o64 = out.astype(np.float64)
+    mids = np.stack([(o64 + up) / 2, (o64 + dn) / 2])
+    near = (np.abs(mids - s64[None]) <= np.spacing(np.abs(s64))[None] * 2).any(0)
+    return out, np.nonzero(near)[0]
+
+
+def test_pcm_decode_is_correctly_rounded_for_every_24_bit_value():
+    """The int32-container decode at 24 bits, for all 2^24 values, equals the
+    reference's f32 division value as f32 / 8388607.0
+    (examples/transcribe_wav.rs:342-348)."""
+    scale = np.float32((1 << 23) - 1)
+    recip = np.float32(1.0) / scale
+    v = np.arange(-(1 << 23), 1 << 23, dtype=np.int64).astype(np.float32)
+    want = v / scale
+    got, hard = _markstein_f64(v, scale, recip)
+    for i in hard:
+        got[i] = _residual_div(v[i], scale, recip)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", range(25, 33))
+def test_pcm_decode_edge_values_at_widths_25_to_32(bits):
+    """Widths past 24 bits: the divisor ((1 << (bits-1)) - 1) as f32 and the
+    sample value as f32 are both rounded first, as the reference computes
+    them; the decode equals correctly rounded f32 division at the edges."""
+    scale = np.float32(float((1 << (bits - 1)) - 1))
+    recip = np.float32(1.0) / scale
+    top = (1 << (bits - 1)) - 1
+    ints = [-(1 << (bits - 1)), -top, -(1 << 24) - 1, -(1 << 24), -1, 0, 1, (1 << 24) - 1, 1 << 24, (1 << 24) + 1,
+            top - 1, top]
+    rng = np.random.default_rng(bits)
+    ints += rng.integers(-(1 << (bits - 1)), 1 << (bits - 1), 200).tolist()
+    for iv in ints:
+        v = np.float32(iv)
+        assert _residual_div(v, scale, recip) == v / scale, (bits, iv)

@@ -247,3 +247,22 @@ def test_f32_noise_envelope_bounds_the_oracle(kind, seed):
     assert np.all(excess <= 8.0 * env)
     # the envelope is small where the signal is strong: it is not a blanket pass
     assert np.median(env) < 2e-5
+
+
+@pytest.mark.parametrize("kind,seed", [("sin", 1), ("speech", 3), ("speech", 8)])
+def test_oracle_misses_the_flat_bar_only_on_near_guard_elements(kind, seed):
+    """Where the f32 oracle itself is outside 1e-4 / 1e-3 of float64, the
+    element's mel energy is at most 1e-6 of its frame's energy (f32 FFT
+    noise by construction); those are exactly the elements the GPU parity
+    check may widen, and the envelope there never exceeds its 5e-3 cap."""
+    from scriptrs_amd import synth
+    a = synth.sinusoids(160_000, seed) if kind == "sin" else synth.speech_like(240_000, seed)[:238_080]
+    r = R.extract(a)
+    o = oracle.extract(a)
+    near = R.near_guard(a)
+    env = R.f32_noise_envelope(a)
+    outside = np.abs(o - r) > 1e-4 + 1e-3 * np.abs(r)
+    assert not (outside & ~near).any()
+    assert np.all(env[~near] == 0.0) and env.max() <= R.ENV_CAP
+    print(f"{kind} {seed}: {int(outside.sum())} oracle elements outside the flat bar, all near-guard "
+          f"({int(near.sum())} near-guard elements)")
