@@ -401,6 +401,12 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
 #pragma unroll
     for (int k1 = 0; k1 < 16; ++k1) X[k1 * kXStride + l] = a[k1];
     wave_lds_sync();
+    // From the transposed reads to the MFMAs the wave runs at raised priority:
+    // it is then on a chain of LDS round trips (transpose, split shuffles,
+    // power rows, MFMA operands), and letting it issue ahead of the SIMD's
+    // other waves, which are in their FFT arithmetic, shortens that chain
+    // (3% on the 1 h workload; raising it for the whole FFT was slower).
+    __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int m1 = 0; m1 < 16; ++m1) a[m1] = X[l * kXStride + m1];
     dft16<false>(a);  // a[k2] = Z[l + 16 k2]
@@ -443,8 +449,10 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     // ---- 3. mel on the matrix cores: block j of chain c accumulates
     // W[64c + 4j + m][k0 + s] . P[frame n][k0 + s] over its steps s, 4 steps
     // (one float4 of A and of B operands) per group; the next group's
-    // operands are loaded while this group's MFMAs issue.
-    f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0;
+    // operands are loaded while this group's MFMAs issue.  Chain 1 alternates
+    // between two accumulators so consecutive MFMAs do not wait on each
+    // other.
+    f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, c2 = c0;
     float4 a1n = mel_a[kChainSteps[0] / 4][lane], b1n = *reinterpret_cast<const float4*>(pb1);
     float4 a0n = mel_a[0][lane], b0n = *reinterpret_cast<const float4*>(pb0);
 #pragma unroll
@@ -460,19 +468,20 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
       }
       c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.x, b1.x, c1, 0, 0, 0);
       if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.x, b0.x, c0, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.y, b1.y, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.y, b1.y, c2, 0, 0, 0);
       if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.y, b0.y, c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.z, b1.z, c1, 0, 0, 0);
       if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.z, b0.z, c0, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.w, b1.w, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.w, b1.w, c2, 0, 0, 0);
       if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.w, b0.w, c0, 0, 0, 0);
       // The group's operands stay allocated past its MFMAs (see mfma_keep).
       __builtin_amdgcn_sched_barrier(0);
       mfma_keep(a1, b1);
       if (v < kChainSteps[0] / 4) mfma_keep(a0, b0);
     }
+    __builtin_amdgcn_s_setprio(0);
     acc0 = c0;
-    acc1 = c1;
+    acc1 = c1 + c2;
     // Every frame of the quad is stored: frames past the item's end land in
     // its last tile's padding, which nothing reads.
     const int q = u - it.unit_off;
