@@ -98,7 +98,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps first: the GPU clock ramps up over the first tens of ms of load")
     ap.add_argument("--workload", default="config3", choices=["config1", "config1host", "config2", "config3", "config4", "config5", "vad1h"])
     ap.add_argument("--pcm", default="f32", choices=["f32", "i16"],
                     help="input samples: f32, or 16-bit PCM decoded in the kernel")

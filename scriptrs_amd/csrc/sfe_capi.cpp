@@ -174,11 +174,11 @@ struct sfe_ctx {
   hipStream_t s_copy = nullptr;
   DevBuf meta;      // Item tables
   std::vector<Item> meta_items;  // host copy of what meta holds (empty: unknown)
-  // End of the previous call's device work.  The next call's stream waits on
-  // it, so calls on one context are ordered even across streams (they share
-  // the item table and the raw scratch).
+  // Orders calls on one context across streams (they share the item table
+  // and the raw scratch): see order_after_last.
   hipEvent_t ev_last = nullptr;
   bool has_last = false;
+  hipStream_t last_stream = nullptr;  // the stream the previous call's device work ran on
   PinBuf h_meta;
   DevBuf scratch;   // raw log-mel in 16-frame tiles, f32 (the normalisation kernel's input)
   DevBuf io_in;     // sfe_extract staging (audio)
@@ -200,6 +200,26 @@ struct sfe_ctx {
 };
 
 namespace {
+
+// Orders this call's work on `stream` after the context's previous call (the
+// calls share the item table and the raw scratch).  On the stream that call
+// used, stream order already does; an event there would cost the device a
+// barrier between the calls' kernels.  On another stream, an event recorded
+// now on the previous call's stream (after everything enqueued there so far,
+// that call included) is waited on.
+hipError_t order_after_last(sfe_ctx* ctx, hipStream_t stream) {
+  if (!ctx->has_last || stream == ctx->last_stream) return hipSuccess;
+  hipError_t e = hipEventRecord(ctx->ev_last, ctx->last_stream);
+  if (e != hipSuccess) return e;
+  return hipStreamWaitEvent(stream, ctx->ev_last, 0);
+}
+
+// The call just enqueued ran on `stream` (no device work is added).
+hipError_t mark_last(sfe_ctx* ctx, hipStream_t stream) {
+  ctx->has_last = true;
+  ctx->last_stream = stream;
+  return hipSuccess;
+}
 
 // Builds the item table for n spans and returns total tiles.
 int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vector<Item>* items,
@@ -277,7 +297,7 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* 
 // the log-mel and normalisation kernels.
 int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, int64_t total_tiles,
               int32_t out_dtype, void* out, hipStream_t stream, int pad_to = 0) {
-  if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(stream, ctx->ev_last, 0));
+  SFE_HIP(order_after_last(ctx, stream));
   const size_t mbytes = items.size() * sizeof(Item);
   // A call with the same item table as the previous upload (repeated plans,
   // equal-sized windows) reuses the device copy.  The table is only read by
@@ -299,8 +319,7 @@ int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, i
   float* raw = static_cast<float*>(ctx->scratch.ptr);
   const int rc = launch_pair(ctx, src, items.data(), d_items, (int)items.size(), raw, out, out_dtype, pad_to, stream);
   if (rc) return rc;
-  SFE_HIP(hipEventRecord(ctx->ev_last, stream));
-  ctx->has_last = true;
+  SFE_HIP(mark_last(ctx, stream));
   return SFE_OK;
 }
 
@@ -693,7 +712,7 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
       frame_offsets[i + 1] = fo;
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(s, ctx->ev_last, 0));
+    SFE_HIP(order_after_last(ctx, s));
     Item* d_items = reinterpret_cast<Item*>(ctx->noalloc);
     float* raw = reinterpret_cast<float*>(ctx->noalloc + sfe::kNoAllocItemBytes);
     SFE_HIP(hipMemcpyAsync(d_items, items, (size_t)n * sizeof(Item), hipMemcpyHostToDevice, s));
@@ -701,8 +720,7 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     ctx->h_meta.pending = true;
     rc = launch_pair(ctx, f32_source(recording), items, d_items, n, raw, out, out_dtype, 0, s, kBoth, false);
     if (rc) return rc;
-    SFE_HIP(hipEventRecord(ctx->ev_last, s));
-    ctx->has_last = true;
+    SFE_HIP(mark_last(ctx, s));
     return SFE_OK;
   });
 }
@@ -728,10 +746,9 @@ int sfe_vad_frames(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int3
     if ((rc = check_ctx(ctx))) return rc;
     std::lock_guard<std::mutex> lock(ctx->mu);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (ctx->has_last) SFE_HIP(hipStreamWaitEvent(s, ctx->ev_last, 0));
+    SFE_HIP(order_after_last(ctx, s));
     SFE_HIP(sfe::launch_vad_frames(src.ptr, src.pcm, src.scale, len, out, s));
-    SFE_HIP(hipEventRecord(ctx->ev_last, s));
-    ctx->has_last = true;
+    SFE_HIP(mark_last(ctx, s));
     return SFE_OK;
   });
 }
@@ -850,10 +867,8 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     if (!pinned)
       for (int b = 0; b < 2; ++b) SFE_HIP(ctx->h_win[b].reserve((size_t)half * es));
     hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
-    if (ctx->has_last) {
-      SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_last, 0));
-      SFE_HIP(hipStreamWaitEvent(sx, ctx->ev_last, 0));
-    }
+    SFE_HIP(order_after_last(ctx, sc));
+    SFE_HIP(order_after_last(ctx, sx));
     memcpy(ctx->h_meta.ptr, items.data(), mbytes);
     SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, sc));
     SFE_HIP(hipEventRecord(ctx->h_meta.ev, sc));
