@@ -305,10 +305,10 @@ def main() -> int:
     return 0
 
 
-def other_configs(ext, args, steps: int = 20) -> dict:
+def other_configs(ext, args, steps: int = 50, warmup: int = 50) -> dict:
     """Wall-clock ms per step of configs 1, 2 and 4 (resident, f32), run
     after the headline workload in the same process: one launch sequence per
-    step, timed over `steps` steps after 3 warmups."""
+    step, timed over `steps` steps after `warmup` untimed ones."""
     import torch
     from scriptrs_amd import TaskTable
     res = {}
@@ -318,7 +318,7 @@ def other_configs(ext, args, steps: int = 20) -> dict:
         tt = TaskTable(tasks)
         dev = torch.from_numpy(x).cuda()
         out = torch.empty(int(tt.frame_offsets[-1]) * 128, dtype=torch.float32, device="cuda")
-        for _ in range(3):
+        for _ in range(warmup):
             ext.extract_chunks(dev, tt, stream=stream, out=out)
         torch.cuda.synchronize()
         t0 = time.perf_counter()

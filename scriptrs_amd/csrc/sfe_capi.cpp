@@ -402,7 +402,11 @@ int64_t sfe_num_frames(const sfe_config* cfg, int64_t len) {
 }
 
 int64_t sfe_max_feature_frames(const sfe_config* cfg) {
-  return cfg->max_audio_samples / cfg->hop_length + 1;
+  sfe_config def;
+  sfe_config_default(&def);
+  const sfe_config* c = cfg ? cfg : &def;
+  const int64_t hop = c->hop_length > 0 ? c->hop_length : sfe::kHop;
+  return c->max_audio_samples < 0 ? 0 : c->max_audio_samples / hop + 1;
 }
 
 int sfe_plan_fast(const sfe_overlap_config* cfg, int64_t audio_len, sfe_chunk* tasks, int32_t cap,
@@ -782,6 +786,10 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
       starts[i] = t.audio_start;
       lens[i] = t.audio_end - t.audio_start;
     }
+    // A window longer than the recording holds no more than the recording:
+    // clamping keeps the device ring and the batch sizes (window_samples
+    // times the sample size and the batch count) from overflowing.
+    window_samples = std::min(window_samples, std::max<int64_t>(len, 1));
     if ((rc = check_ctx(ctx))) return rc;
     std::lock_guard<std::mutex> lock(ctx->mu);
     std::vector<Item> items;

@@ -316,3 +316,12 @@ def test_pcm_decode_edge_values_at_widths_25_to_32(bits):
     for iv in ints:
         v = np.float32(iv)
         assert _residual_div(v, scale, recip) == v / scale, (bits, iv)
+
+
+def test_max_feature_frames_null_and_zero_hop():
+    L = _lib.lib()
+    assert L.sfe_max_feature_frames(None) == 1501
+    c = _lib.SfeConfig()
+    L.sfe_config_default(ctypes.byref(c))
+    c.hop_length = 0
+    assert L.sfe_max_feature_frames(ctypes.byref(c)) == 240_000 // 160 + 1

@@ -547,3 +547,18 @@ def test_contexts_on_concurrent_host_threads():
     for (k, r), (out, fo) in results.items():
         assert np.array_equal(fo, wfo), (k, r)
         assert torch.equal(out, want), (k, r)
+
+
+def test_streamed_window_far_longer_than_recording(extractor):
+    """A window of 2^40 samples is clamped to the recording: the device ring
+    and batch sizes stay small, and the result equals the resident path."""
+    import torch
+    from scriptrs_amd import build_fast_execution_plan
+    _flush("case: streamed, window 2^40 samples")
+    rec = synth.speech_like(700_000, 13)
+    tasks = build_fast_execution_plan(rec.size)
+    a, fa = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+    b, fb = extractor.extract_chunks_streamed(rec, tasks, window_samples=1 << 40)
+    torch.cuda.synchronize()
+    assert np.array_equal(fa, fb)
+    assert torch.equal(a, b)
