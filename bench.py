@@ -288,9 +288,10 @@ def main() -> int:
         result["parity"] = {"max_abs_err_vs_oracle": float(np.nanmax(err)),
                             "frac_within_1e-4_abs_1e-3_rel": float(ok.mean()),
                             "outside_flat_bar": int((~ok).sum())}
-        # Every element outside the flat bar should be near the f32 noise
-        # floor (float64 mel energy at most 1e-6 of its frame's energy), as
-        # the GPU parity tests require (tests/parity.py).
+        # Every element outside the flat bar should have a non-zero f32 noise
+        # envelope (a near-guard element, float64 mel energy at most 1e-6 of
+        # its frame's energy, or a row holding one), as the GPU parity tests
+        # require (tests/parity.py).
         if x.dtype == np.float32 and args.dtype == "f32":
             sys.path.insert(0, os.path.join(ROOT, "tests"))
             import np_reference as R
@@ -298,8 +299,8 @@ def main() -> int:
             near = np.zeros(want.size, bool)
             for i in range(len(starts)):
                 a = x[int(starts[i]):int(starts[i] + lens[i])]
-                near[128 * fo[i]:128 * fo[i + 1]] = R.near_guard(a).reshape(-1)
-            result["parity"]["outside_flat_bar_all_near_guard"] = bool(not (~ok & ~near).any())
+                near[128 * fo[i]:128 * fo[i + 1]] = (R.f32_noise_envelope(a) > 0).reshape(-1)
+            result["parity"]["outside_flat_bar_all_in_envelope"] = bool(not (~ok & ~near).any())
     print(json.dumps(result), flush=True)
     ext.close()
     return 0

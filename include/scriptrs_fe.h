@@ -247,7 +247,16 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
                                     int32_t bits_per_sample, int64_t len, const sfe_chunk* tasks, int32_t n,
                                     int32_t out_dtype, void* out, int64_t* frame_offsets, int64_t window_samples);
 
-/* ---- instrumentation (no reference counterpart) ----------------------- */
+/* ---- tuning and instrumentation (no reference counterpart) ----------- */
+
+/* Shared frames: on by default.  Overlapping chunk tasks of one call
+ * (sfe_extract_chunks, _pcm, _padded, sfe_extract_batch) whose starts agree
+ * modulo the hop have identical log-mel for the frames that lie inside both
+ * (at least one sample inside each task's ends); those are computed once
+ * and each task keeps its first and last 4-frame groups.  The output is
+ * bitwise the same either way; turning it off makes every task compute all
+ * of its frames (the streamed and allocation-free entry points always do). */
+int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
 
 /* Turn per-kernel timing on or off for ctx.  When on, every launch of the
  * log-mel and normalisation kernels is bracketed by HIP events on the stream

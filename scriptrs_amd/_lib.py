@@ -21,7 +21,7 @@ EXPORTS = (
     "sfe_plan_fast", "sfe_build_tables", "sfe_last_error", "sfe_create", "sfe_destroy", "sfe_extract",
     "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_pcm",
     "sfe_extract_chunks_padded", "sfe_extract_chunks_streamed", "sfe_extract_chunks_streamed_pcm",
-    "sfe_set_timing", "sfe_get_timing", "sfe_vad_num_windows", "sfe_vad_frames", "sfe_extract_chunks_noalloc",
+    "sfe_set_frame_sharing", "sfe_set_timing", "sfe_get_timing", "sfe_vad_num_windows", "sfe_vad_frames", "sfe_extract_chunks_noalloc",
 )
 
 
@@ -88,6 +88,7 @@ def lib() -> ctypes.CDLL:
         "sfe_extract_chunks_streamed": (ctypes.c_int, [vp, fp, i64, P(SfeChunk), i32, i32, vp, i64p, i64]),
         "sfe_vad_num_windows": (i64, [i64]),
         "sfe_vad_frames": (ctypes.c_int, [vp, vp, i32, i32, i64, vp, i64, vp]),
+        "sfe_set_frame_sharing": (ctypes.c_int, [vp, i32]),
         "sfe_set_timing": (ctypes.c_int, [vp, i32]),
         "sfe_get_timing": (ctypes.c_int, [vp, P(ctypes.c_double), P(ctypes.c_double), P(i32)]),
     }

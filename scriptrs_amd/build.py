@@ -35,6 +35,7 @@ SOURCES = [
     ("sfe_noalloc.hip", ["-x", "hip"]),
     # bit-exact table construction: every f32/f64 op rounded separately
     ("sfe_tables.cpp", ["-x", "hip", "-ffp-contract=off"]),
+    ("sfe_share.cpp", ["-x", "hip"]),
     ("sfe_capi.cpp", ["-x", "hip"]),
 ]
 

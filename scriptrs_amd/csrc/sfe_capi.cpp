@@ -189,6 +189,9 @@ struct sfe_ctx {
   PinBuf h_win[2];
   hipEvent_t ev_copied[2] = {nullptr, nullptr};
   hipEvent_t ev_done[2] = {nullptr, nullptr};
+  // Frames that overlapping chunk tasks share are computed once
+  // (sfe_set_frame_sharing).
+  bool share = true;
   // kernel timing (sfe_set_timing): events around each launch, summed on read
   bool timing = false;
   std::vector<hipEvent_t> tev;  // pairs: start, end; kind alternates logmel, norm
@@ -231,13 +234,8 @@ int build_items(const int64_t* starts, const int64_t* lens, int32_t n, std::vect
     if (lens[i] <= 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty (item " + std::to_string(i) + ")");
     const int64_t T = lens[i] / sfe::kHop + 1;
     if (T > INT32_MAX / 2) return fail(SFE_INVALID_ARG, "item too long");
-    Item& it = (*items)[i];
-    it.start = starts[i];
-    it.len = lens[i];
-    it.out_off = (int64_t)sfe::kRawTile * tiles;  // raw scratch: whole 16-frame tiles per item
-    it.dst_off = (int64_t)sfe::kMel * fo;
-    it.T = (int32_t)T;
-    it.unit_off = (int32_t)units;
+    (*items)[i] = sfe::own_item(starts[i], lens[i], (int64_t)sfe::kRawTile * tiles, (int64_t)sfe::kMel * fo,
+                                (int32_t)units);
     fo += T;
     tiles += sfe::tiles_for(T);
     units += sfe::units_for(T);
@@ -269,55 +267,70 @@ hipEvent_t timing_event(sfe_ctx* ctx) {
 // bandwidth from it.)
 enum Stages { kLogmel = 1, kNorm = 2, kBoth = 3 };
 
-int launch_pair(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d_items, int n, float* raw,
-                void* out, int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth,
-                bool allow_timing = true) {
-  if (n <= 0) return SFE_OK;
-  const int u0 = items[0].unit_off;
-  const int u1 = items[n - 1].unit_off + (int)sfe::units_for(items[n - 1].T);
+int launch_pair(sfe_ctx* ctx, const Source& src, const Item* lm, const Item* d_lm, int n_lm, const Item* norm,
+                const Item* d_norm, int n_norm, float* raw, void* out, int32_t out_dtype, int pad_to,
+                hipStream_t stream, int stages = kBoth, bool allow_timing = true) {
+  if (n_lm <= 0 && n_norm <= 0) return SFE_OK;
+  const int u0 = n_lm > 0 ? lm[0].unit_off : 0;
+  const int u1 = n_lm > 0 ? lm[n_lm - 1].unit_off + lm[n_lm - 1].n_units : 0;
   int max_T = 0;
-  for (int i = 0; i < n; ++i) max_T = std::max(max_T, (int)items[i].T);
+  for (int i = 0; i < n_norm; ++i) max_T = std::max(max_T, (int)norm[i].T);
   hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
   if (ctx->timing && allow_timing)
     for (int i = 0; i < 4; ++i)
       if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
   if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
   if (stages & kLogmel)
-    SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_items, n, u0, u1 - u0, ctx->d_tables,
+    SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_lm, n_lm, u0, u1 - u0, ctx->d_tables,
                                ctx->cfg.preemphasis, raw, ctx->grid_cap, stream));
   if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
   if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
   if (stages & kNorm)
-    SFE_HIP(sfe::launch_norm(raw, d_items, n, max_T, pad_to, out, out_dtype == SFE_BF16, stream));
+    SFE_HIP(sfe::launch_norm(raw, d_norm, n_norm, max_T, pad_to, out, out_dtype == SFE_BF16, stream));
   if (e[3]) SFE_HIP(hipEventRecord(e[3], stream));
   return SFE_OK;
 }
 
+// launch_pair over one table that both kernels read (items with their own
+// regions).
+int launch_own(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d_items, int n, float* raw, void* out,
+               int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth, bool allow_timing = true) {
+  return launch_pair(ctx, src, items, d_items, n, items, d_items, n, raw, out, out_dtype, pad_to, stream, stages,
+                     allow_timing);
+}
+
 // Uploads items through the pinned staging buffer on `stream`, then runs
 // the log-mel and normalisation kernels.
-int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, int64_t total_tiles,
-              int32_t out_dtype, void* out, hipStream_t stream, int pad_to = 0) {
+int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, int32_t out_dtype, void* out,
+              hipStream_t stream, int pad_to = 0) {
   SFE_HIP(order_after_last(ctx, stream));
-  const size_t mbytes = items.size() * sizeof(Item);
-  // A call with the same item table as the previous upload (repeated plans,
+  std::vector<Item> lm, norm;
+  const int64_t total_tiles = sfe::plan_items(items.data(), (int)items.size(), ctx->share, &lm, &norm);
+  // one table: the log-mel entries, then the normalisation entries
+  const size_t n_lm = lm.size();
+  lm.insert(lm.end(), norm.begin(), norm.end());
+  const std::vector<Item>& table = lm;
+  const size_t mbytes = table.size() * sizeof(Item);
+  // A call with the same table as the previous upload (repeated plans,
   // equal-sized windows) reuses the device copy.  The table is only read by
   // the kernels, so earlier work still in flight is unaffected.
-  const bool same = ctx->meta.ptr && ctx->meta_items.size() == items.size() &&
-                    memcmp(ctx->meta_items.data(), items.data(), mbytes) == 0;
+  const bool same = ctx->meta.ptr && ctx->meta_items.size() == table.size() &&
+                    memcmp(ctx->meta_items.data(), table.data(), mbytes) == 0;
   if (!same) {
     ctx->meta_items.clear();
     SFE_HIP(ctx->h_meta.reserve(mbytes));
     SFE_HIP(ctx->meta.reserve(mbytes));
-    memcpy(ctx->h_meta.ptr, items.data(), mbytes);
+    memcpy(ctx->h_meta.ptr, table.data(), mbytes);
     SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, stream));
     SFE_HIP(hipEventRecord(ctx->h_meta.ev, stream));
     ctx->h_meta.pending = true;
-    ctx->meta_items = items;
+    ctx->meta_items = table;
   }
-  const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
+  const Item* d_table = static_cast<const Item*>(ctx->meta.ptr);
   SFE_HIP(ctx->scratch.reserve((size_t)total_tiles * sfe::kRawTile * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
-  const int rc = launch_pair(ctx, src, items.data(), d_items, (int)items.size(), raw, out, out_dtype, pad_to, stream);
+  const int rc = launch_pair(ctx, src, table.data(), d_table, (int)n_lm, table.data() + n_lm, d_table + n_lm,
+                             (int)items.size(), raw, out, out_dtype, pad_to, stream);
   if (rc) return rc;
   SFE_HIP(mark_last(ctx, stream));
   return SFE_OK;
@@ -551,7 +564,7 @@ int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64
     std::vector<Item> items;
     int64_t start = 0, tiles = 0, fo[2];
     if ((rc = build_items(&start, &len, 1, &items, fo, &tiles))) return rc;
-    if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, tiles, SFE_F32, ctx->io_out.ptr, s)))
+    if ((rc = run_items(ctx, f32_source(static_cast<float*>(ctx->io_in.ptr)), items, SFE_F32, ctx->io_out.ptr, s)))
       return rc;
     SFE_HIP(hipMemcpyAsync(ctx->h_io_out.ptr, ctx->io_out.ptr, out_bytes, hipMemcpyDeviceToHost, s));
     SFE_HIP(hipStreamSynchronize(s));
@@ -595,7 +608,7 @@ int sfe_extract_batch(sfe_ctx* ctx, const float* samples, const int64_t* offsets
     std::vector<Item> items;
     int64_t tiles = 0;
     if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-    return run_items(ctx, f32_source(samples), items, tiles, out_dtype, out,
+    return run_items(ctx, f32_source(samples), items, out_dtype, out,
                      static_cast<hipStream_t>(stream));
   });
 }
@@ -627,7 +640,7 @@ int sfe_extract_chunks_pcm(sfe_ctx* ctx, const void* recording, int32_t pcm_form
     std::vector<Item> items;
     int64_t tiles = 0;
     if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
-    return run_items(ctx, src, items, tiles, out_dtype, out, static_cast<hipStream_t>(stream));
+    return run_items(ctx, src, items, out_dtype, out, static_cast<hipStream_t>(stream));
   });
 }
 
@@ -661,7 +674,7 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
       items[i].dst_off = (int64_t)i * sfe::kMel * target_frames;
       feature_frames[i] = items[i].T;
     }
-    return run_items(ctx, f32_source(recording), items, tiles, out_dtype, out, static_cast<hipStream_t>(stream),
+    return run_items(ctx, f32_source(recording), items, out_dtype, out, static_cast<hipStream_t>(stream),
                      target_frames);
   });
 }
@@ -704,12 +717,8 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     frame_offsets[0] = 0;
     for (int32_t i = 0; i < n; ++i) {
       Item& it = items[i];
-      it.start = tasks[i].audio_start;
-      it.len = tasks[i].audio_end - tasks[i].audio_start;
-      it.T = (int32_t)(it.len / sfe::kHop + 1);
-      it.out_off = (int64_t)sfe::kRawTile * tiles;
-      it.dst_off = (int64_t)sfe::kMel * fo;
-      it.unit_off = (int32_t)units;
+      it = sfe::own_item(tasks[i].audio_start, tasks[i].audio_end - tasks[i].audio_start, (int64_t)sfe::kRawTile * tiles,
+                         (int64_t)sfe::kMel * fo, (int32_t)units);
       fo += it.T;
       tiles += sfe::tiles_for(it.T);
       units += sfe::units_for(it.T);
@@ -722,7 +731,7 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     SFE_HIP(hipMemcpyAsync(d_items, items, (size_t)n * sizeof(Item), hipMemcpyHostToDevice, s));
     SFE_HIP(hipEventRecord(ctx->h_meta.ev, s));
     ctx->h_meta.pending = true;
-    rc = launch_pair(ctx, f32_source(recording), items, d_items, n, raw, out, out_dtype, 0, s, kBoth, false);
+    rc = launch_own(ctx, f32_source(recording), items, d_items, n, raw, out, out_dtype, 0, s, kBoth, false);
     if (rc) return rc;
     SFE_HIP(mark_last(ctx, s));
     return SFE_OK;
@@ -910,7 +919,7 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
       SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[e], 0));
       const int32_t first = groups[bt.g0].first;
       const int32_t end = groups[bt.g1 - 1].first + groups[bt.g1 - 1].count;
-      rc = launch_pair(ctx, rsrc, items.data() + first, d_items + first, end - first, raw, out, out_dtype, 0, sc,
+      rc = launch_own(ctx, rsrc, items.data() + first, d_items + first, end - first, raw, out, out_dtype, 0, sc,
                        kLogmel);
       if (rc) return rc;
       SFE_HIP(hipEventRecord(ctx->ev_done[e], sc));
@@ -919,7 +928,7 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
       // batch: one launch over many items instead of many launches over a few.
       norm_windows += bt.g1 - bt.g0;
       if (bi + 1 == batches.size() || norm_windows >= kStreamNormWindows) {
-        rc = launch_pair(ctx, rsrc, items.data() + norm_first, d_items + norm_first, end - norm_first, raw, out,
+        rc = launch_own(ctx, rsrc, items.data() + norm_first, d_items + norm_first, end - norm_first, raw, out,
                          out_dtype, 0, sc, kNorm);
         if (rc) return rc;
         norm_first = end;
@@ -931,6 +940,13 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     ctx->has_last = false;  // everything has completed
     return SFE_OK;
   });
+}
+
+int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable) {
+  if (!ctx) return fail(SFE_INVALID_ARG, "null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->share = enable != 0;
+  return SFE_OK;
 }
 
 int sfe_set_timing(sfe_ctx* ctx, int32_t enable) {

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace sfe {
 
 // Shape the kernels are specialised to: TranscriptionConfig::default()
@@ -29,21 +31,77 @@ constexpr int kMelVec = kMelSteps / 4;  // float4 A operands per lane
 static_assert(kChainSteps[0] + kChainSteps[1] == kMelSteps && kChainSteps[0] % 4 == 0 && kChainSteps[1] % 4 == 0,
               "chains are whole float4 steps");
 
-// One featurized item: a clip or a long-form chunk task.  samples[start,
-// start+len) is featurized into out[dst_off + m*S + t] (S = T, or the
-// padded row length of the encoder-input layout).  The raw log-mel (log2;
-// times ln 2 is the log-mel) goes to scratch in tiles of 16 frames: tile
-// t / 16 of the item at raw[out_off + 2048 * (t / 16)], holding 8 slabs of
-// 16 features, each [16 frames][16 features], slab s holding features
-// 16s..16s+15.
+// Raw log-mel (log2; times ln 2 is the log-mel) lives in scratch in tiles
+// of 16 frames (kRawTile floats): 8 slabs of 16 features, each [16 frames]
+// [16 features], slab s holding features 16s..16s+15.  Frame f of a region
+// whose tile 0 holds frames 0..15 sits at region + raw_frame(f).
+constexpr int kTile = 16;              // frames per raw tile
+constexpr int kRawTile = kTile * 128;  // raw scratch floats per tile of 16 frames
+constexpr int kQuad = 4;               // frames per unit of work (one wave pass) of the log-mel kernel
+__host__ __device__ constexpr int64_t raw_frame(int64_t f) { return kRawTile * (f >> 4) + 16 * (f & 15); }
+
+// One entry of either kernel's table.
+//
+// Log-mel entries: frames 4 q0 .. 4 (q0 + n_units) - 1 of samples[start,
+// start + len) (preemphasis restarting at `start`, zero padding outside),
+// frame f written to raw[out_off + raw_frame(f)]; its units (4-frame quads)
+// are numbered from unit_off.  Entries are whole items, or parts of them
+// (first or last quads), or spans that several overlapping items share.
+//
+// Normalisation entries, one per featurized item (a clip or a long-form
+// chunk task) of T frames, written to out[dst_off + m*S + t] (S = T, or the
+// padded row length of the encoder-input layout).  Frame f of its raw
+// log-mel is read from raw[grid_off + raw_frame(f + gshift)] for f in
+// [f_lo, f_hi], raw[tail_off + raw_frame(f)] past f_hi and raw[out_off +
+// raw_frame(f)] below f_lo.  An item with its own region has f_lo = 0,
+// f_hi = T - 1, grid_off = out_off and gshift = 0.
 struct Item {
   int64_t start;
   int64_t len;
-  int64_t out_off;   // raw (scratch) element offset: kRawTile * (tiles of the items before it)
-  int64_t dst_off;   // output element offset: out_off when packed, i * feature_size * pad_to when padded
+  int64_t out_off;
+  int64_t dst_off;
+  int64_t grid_off;
+  int64_t tail_off;
   int32_t T;         // len / hop + 1
-  int32_t unit_off;  // first unit (4-frame quad) of this item, relative to the launch
+  int32_t unit_off;  // log-mel: first unit, relative to the launch
+  int32_t n_units;   // log-mel: units of the entry
+  int32_t q0;        // log-mel: first quad of the entry within its frames
+  int32_t f_lo, f_hi, gshift;
+  int32_t pad_;
 };
+static_assert(sizeof(Item) == 80, "item table layout");
+
+// An item with its own raw region at out_off (both kernels' view).
+inline Item own_item(int64_t start, int64_t len, int64_t out_off, int64_t dst_off, int32_t unit_off) {
+  Item it{};
+  it.start = start;
+  it.len = len;
+  it.out_off = out_off;
+  it.dst_off = dst_off;
+  it.grid_off = out_off;
+  it.tail_off = out_off;
+  it.T = (int32_t)(len / kHop + 1);
+  it.unit_off = unit_off;
+  it.n_units = (int32_t)((it.T + kQuad - 1) / kQuad);
+  it.q0 = 0;
+  it.f_lo = 0;
+  it.f_hi = it.T - 1;
+  it.gshift = 0;
+  return it;
+}
+
+// Shared frames (sfe_share.cpp).  Frames of overlapping items whose samples
+// lie at least one sample inside each item and whose starts agree modulo the
+// hop are computed once: items' own regions keep only their first quad and
+// their last quads, and a shared log-mel entry per run of such items covers
+// the union of their interior frames.  Given items with their own regions
+// (own_item; out_off ignored), fills the log-mel and normalisation tables
+// and returns the raw tiles they use.  With share = false, or where sharing
+// saves no quads, every item keeps its own region.
+int64_t plan_items(const Item* items, int n, bool share, std::vector<Item>* lm, std::vector<Item>* norm);
+// Frames of one run's shared entry at most (512 MB of raw log-mel): an
+// item's first and last tiles follow its run's shared region, within 4 GB.
+constexpr int64_t kMaxShareFrames = (int64_t)1 << 20;
 
 // Constant tables, uploaded once per context.
 struct DevTables {
@@ -65,9 +123,6 @@ void mel_filterbank(int n_fft, int n_mels, int sample_rate, float* out);
 bool build_dev_tables(int sample_rate, DevTables* t);
 
 // Kernel launchers (sfe_kernels.hip).  All asynchronous on `stream`.
-constexpr int kTile = 16;  // frames per raw tile
-constexpr int kRawTile = kTile * 128;  // raw scratch floats per tile of 16 frames
-constexpr int kQuad = 4;   // frames per unit of work (one wave pass) of the log-mel kernel
 int64_t tiles_for(int64_t T);
 int64_t units_for(int64_t T);  // quads of an item: ceil(T / 4)
 // grid_cap: workgroups resident on the device at once (the kernel loops

@@ -147,7 +147,7 @@ struct Span {
 
 template <typename S>
 __device__ __forceinline__ Span<S> make_span(const Item& it, const S* samples, int u) {
-  const int fw = (u - it.unit_off) * kQuad;
+  const int fw = (u - it.unit_off + it.q0) * kQuad;
   Span<S> sp;
   sp.s0 = (int64_t)fw * kHop - kPad;
   sp.jlo = sp.s0 < 0 ? (int)(-sp.s0) : 0;
@@ -484,8 +484,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     acc1 = c1 + c2;
     // Every frame of the quad is stored: frames past the item's end land in
     // its last tile's padding, which nothing reads.
-    const int q = u - it.unit_off;
-    pend = it.out_off + (int64_t)kRawTile * (q >> 2) + 64 * (q & 3);
+    pend = it.out_off + raw_frame((int64_t)(u - it.unit_off + it.q0) * kQuad);
   }
   if (pend >= 0) {
     float* o = out + pend;
@@ -730,17 +729,42 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   const int slab = (work % S::kSlabs) * F;
   const Item it = items[item];
   const int T = it.T;
-  // Uniform bases with 32-bit lane offsets.  Raw tiles hold 16 frames, each
-  // slab 1 KB frame-major inside: frame f of this slab sits at
-  // xb + kRawTile * (f / 16) + 16 * (f % 16).
+  // Frame f of the item, features 4 q .. 4 q + 3 of this slab: from the
+  // shared region for f in [f_lo, f_hi], else from the item's own first or
+  // last tiles (raw_frame: 16-frame tiles, the slab 1 KB frame-major inside).
   static_assert(F == 16 && S::kGroup == 16, "one wave's load covers one tile of one slab");
-  const float* xb = raw + it.out_off + 256 * (slab / 16);
+  // Loads address a uniform base (the start of the item's shared frames,
+  // this slab) plus a 32-bit per-lane byte offset: an item's own first and
+  // last tiles come after its shared region, which holds at most
+  // kMaxShareFrames frames, and an item with its own region has all three
+  // at out_off.  The region is chosen by adding differences under
+  // conditions (a choice among several values compiles to a table in
+  // private memory).  The own first tile holds frames below f_lo <= 16, so
+  // only round 0 can reach it.
+  const int f_lo = it.f_lo, f_hi = it.f_hi;
+  const char* bg = reinterpret_cast<const char*>(raw + it.grid_off + 256 * (slab / 16));
+  // Frame 0 is always at out_off: below f_lo for an item that shares
+  // frames, and an item with its own region has grid_off = out_off.
+  const float4* p0 = reinterpret_cast<const float4*>(raw + it.out_off + 256 * (slab / 16) + 4 * q);
+  // This lane's frame in round j is fr + kSpan j, kSpan / 16 tiles on from
+  // round 0 in whichever region holds it.
+  static_assert(kSpan % 16 == 0 && kSpan > 16, "rounds are whole tiles, past the own first tile");
+  constexpr uint32_t kRound = 4u * kRawTile * (kSpan / 16);  // bytes
+  const uint32_t og = 4u * (uint32_t)(raw_frame(fr + it.gshift) + 4 * q);
+  const uint32_t dlo = 4u * (uint32_t)(it.out_off - it.grid_off + raw_frame(fr) - raw_frame(fr + it.gshift));
+  const uint32_t dhi = 4u * (uint32_t)(it.tail_off - it.grid_off + raw_frame(fr) - raw_frame(fr + it.gshift));
+  const int flo = f_lo - fr, fhi = f_hi - fr;  // round j holds frame fr + kSpan j
+  auto round = [og, dlo, dhi, flo, fhi, bg](int j) -> const float4* {
+    const int d = kSpan * j;
+    uint32_t o = og + kRound * (uint32_t)j + (d > fhi ? dhi : 0u);
+    if (j == 0) o += flo > 0 ? dlo : 0u;
+    return reinterpret_cast<const float4*>(bg + o);
+  };
   const int rs = pad_to > 0 ? pad_to : T;  // output row length
   O* ob = out + it.dst_off + (size_t)slab * rs;
   if (pad_to > 0) zero_tail<W, F>(ob, T, rs, lane, w);
-  const uint32_t lo = (uint32_t)((fr / 16) * kRawTile + (fr % 16) * 16 + 4 * q);
   const int nr = fr < T ? (T - 1 - fr) / kSpan + 1 : 0;  // rounds holding a frame of this lane
-  const float4 x0 = ln2_scale(*reinterpret_cast<const float4*>(xb + 4 * q));
+  const float4 x0 = ln2_scale(*p0);
 
   double s[4] = {0.0, 0.0, 0.0, 0.0}, sq[4] = {0.0, 0.0, 0.0, 0.0};
   bool eq[4] = {true, true, true, true};
@@ -751,10 +775,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
       // reread the lane's first frame), selected afterwards: a load under a
       // branch waits for itself, and the rounds would load one at a time.
 #pragma unroll
-      for (int j = 0; j < N; ++j) {
-        const size_t off = j < nr ? (size_t)j * (kSpan / 16 * kRawTile) + lo : (size_t)lo;
-        v[j] = *reinterpret_cast<const float4*>(xb + (nr > 0 ? off : (size_t)(4 * q)));
-      }
+      for (int j = 0; j < N; ++j) v[j] = *(j < nr ? round(j) : (nr > 0 ? round(0) : p0));
 #pragma unroll
       for (int j = 0; j < N; ++j) v[j] = j < nr ? ln2_scale(v[j]) : x0;  // x0 padding keeps the constancy test exact
 #pragma unroll
@@ -811,7 +832,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int j = j0 + g < nr ? j0 + g : j0;  // in bounds; unused when past the item
-      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan / 16 * kRawTile) + lo));
+      e[g] = ln2_scale(*round(j));
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -836,7 +857,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int j = j0 + g < nr ? j0 + g : j0;  // in bounds; unused when past the item
-      e[g] = ln2_scale(*reinterpret_cast<const float4*>(xb + (size_t)j * (kSpan / 16 * kRawTile) + lo));
+      e[g] = ln2_scale(*round(j));
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -858,7 +879,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     for (int jr = 0; jr < 4; ++jr) {
       // past the item: the item's first frame (always in bounds), unused
       const int j = 4 * ch + jr;
-      e[jr] = ln2_scale(*reinterpret_cast<const float4*>(xb + (j < nr ? (size_t)j * (kSpan / 16 * kRawTile) + lo : (size_t)(4 * q))));
+      e[jr] = ln2_scale(*(j < nr ? round(j) : p0));
     }
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr)

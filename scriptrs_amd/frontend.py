@@ -173,6 +173,11 @@ class ParakeetFeatureExtractor:
         except Exception:
             pass
 
+    def set_frame_sharing(self, enable: bool) -> None:
+        """Overlapping chunk tasks of one call compute the frames they share
+        once (on by default; the output is bitwise the same either way)."""
+        _check(_lib.lib().sfe_set_frame_sharing(self._handle(), 1 if enable else 0))
+
     def num_frames(self, length: int) -> int:
         return length // self.config.hop_length + 1
 

@@ -118,7 +118,7 @@ def near_guard(audio: np.ndarray) -> np.ndarray:
     return ((mel <= NEAR_GUARD_RATIO * E) & (E > 0)).T
 
 
-def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
+def f32_noise_envelope(audio: np.ndarray, parts: bool = False):
     """Per-element scale of the rounding noise any f32 FFT-based implementation
     of the front end carries, in normalised units, [128, T].
 
@@ -127,9 +127,16 @@ def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
     |X_k|^2 by about 2|X_k| dX + dX^2, the mel value by the filter-weighted
     sum of that, the log by dmel / (mel + 2^-24), and the normalised output
     by that divided by the row's std.  A floor of 4u*|raw| covers the f32 log
-    and elementwise rounding.  The envelope is zero except on near-guard
-    elements (near_guard) and at most ENV_CAP: only those elements may be
-    widened past the flat bar."""
+    and elementwise rounding.  This element term is zero except on near-guard
+    elements (near_guard) and at most ENV_CAP.
+
+    The row term: a row's mean and std are taken over its near-guard
+    elements too, so their noise dx (the element term in raw units) shifts
+    every normalised value z of the row by up to (mean(dx) + |z| *
+    mean(|x - mean| dx) / std) / std (first order in dx: out = (x - mean) /
+    std).  It is zero in rows without near-guard elements and at most
+    ENV_CAP.  Only elements with a non-zero envelope may be widened past the
+    flat bar.  Returns elem + row, or (elem, row) with parts."""
     frames = _frames_f64(audio)
     fb = slaney_mel_filterbank()
     T = frames.shape[0]
@@ -143,5 +150,15 @@ def f32_noise_envelope(audio: np.ndarray) -> np.ndarray:
     std = raw.std(axis=0, ddof=1, keepdims=True) if T > 1 else np.ones((1, raw.shape[1]))
     E = (X ** 2).sum(1, keepdims=True)
     near = (mel <= NEAR_GUARD_RATIO * E) & (E > 0)
-    env = np.where(near, np.minimum(d_raw / std, ENV_CAP), 0.0)
-    return env.T
+    with np.errstate(divide="ignore", invalid="ignore"):
+        elem = np.where(near, np.minimum(d_raw / std, ENV_CAP), 0.0)
+        row = np.zeros_like(elem)
+        if T > 1:
+            dx = elem * std  # raw units
+            dev = np.abs(raw - raw.mean(axis=0, keepdims=True))
+            dm = dx.mean(axis=0, keepdims=True)
+            ds = (dev * dx).mean(axis=0, keepdims=True) / std
+            row = np.where(dx.any(axis=0, keepdims=True), np.minimum((dm + dev / std * ds) / std, ENV_CAP), 0.0)
+    elem = np.nan_to_num(elem, nan=0.0)
+    row = np.nan_to_num(row, nan=0.0)
+    return (elem.T, row.T) if parts else (elem + row).T

@@ -569,3 +569,59 @@ def test_streamed_window_far_longer_than_recording(extractor):
     torch.cuda.synchronize()
     assert np.array_equal(fa, fb)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("seed", [606, 707])
+def test_shared_frames_equal_own_frames(extractor, seed):
+    """Frames that overlapping hop-aligned tasks share are computed once
+    (the default); the output is bitwise what every task computing its own
+    frames gives, for nested, duplicated and partly overlapping tasks, in f32,
+    bf16 and the padded encoder-input layout, and matches the oracle."""
+    import torch
+    from scriptrs_amd import ChunkTask
+    _flush(f"case: shared frames seed {seed}")
+    rng = np.random.default_rng(seed)
+    rec = synth.speech_like(3_000_000, seed)
+    tasks = []
+    for _ in range(40):
+        n = int(rng.integers(1, 240_001))
+        s = 160 * int(rng.integers(0, (rec.size - n) // 160 + 1))
+        tasks.append(ChunkTask(s, s + n, s, 0))
+    tasks += tasks[:4] + [ChunkTask(tasks[5].audio_start + 3200, tasks[5].audio_start + 3200 + 50_000, 0, 0)]
+    dev = torch.from_numpy(rec).cuda()
+    try:
+        got = {}
+        for share in (True, False):
+            extractor.set_frame_sharing(share)
+            got[share] = [extractor.extract_chunks(dev, tasks, dtype=d)[0] for d in ("f32", "bf16")]
+            got[share].append(extractor.extract_chunks_encoder_input(dev, tasks, target_frames=1501)[0])
+        torch.cuda.synchronize()
+    finally:
+        extractor.set_frame_sharing(True)
+    for a, b in zip(got[True], got[False]):
+        assert torch.equal(a, b)
+    out = got[True][0].cpu().numpy()
+    fo = np.concatenate([[0], np.cumsum([(t.audio_end - t.audio_start) // 160 + 1 for t in tasks])])
+    for i, t in enumerate(tasks[:12]):
+        a = rec[t.audio_start:t.audio_end]
+        g = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert_parity(g, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"task {i}")
+
+
+def test_config3_shared_frames_equal_own_frames(extractor):
+    """Config 3 at full size: the 280 chunks with their ~2 s overlaps
+    computed once give bitwise the output of every chunk on its own."""
+    import torch
+    from scriptrs_amd import TaskTable, build_fast_execution_plan
+    _flush("case: config 3 shared frames")
+    rec = synth.speech_like(57_600_000, 3)
+    tasks = TaskTable(build_fast_execution_plan(rec.size))
+    dev = torch.from_numpy(rec).cuda()
+    try:
+        a, _ = extractor.extract_chunks(dev, tasks)
+        extractor.set_frame_sharing(False)
+        b, _ = extractor.extract_chunks(dev, tasks)
+        torch.cuda.synchronize()
+    finally:
+        extractor.set_frame_sharing(True)
+    assert torch.equal(a, b)

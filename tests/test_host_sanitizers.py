@@ -1,5 +1,5 @@
 """The C ABI's host logic under AddressSanitizer + UndefinedBehaviorSanitizer
-(no GPU needed): sfe_capi.cpp and sfe_tables.cpp are rebuilt with the
+(no GPU needed): sfe_capi.cpp, sfe_share.cpp and sfe_tables.cpp are rebuilt with the
 sanitizers on their host pass only (hipcc -Xarch_host -fsanitize=...), linked
 with the kernel objects that build() produced, and driven by
 tests/host_sanitizer_driver.cpp: tables, the planner over lengths up to 8 h,
@@ -29,7 +29,7 @@ def test_host_logic_under_asan_ubsan(tmp_path):
              "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
              "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=all"]
     objs = []
-    for src, extra in (("sfe_capi.cpp", []), ("sfe_tables.cpp", ["-ffp-contract=off"])):
+    for src, extra in (("sfe_capi.cpp", []), ("sfe_share.cpp", []), ("sfe_tables.cpp", ["-ffp-contract=off"])):
         o = str(tmp_path / (src + ".o"))
         subprocess.run([HIPCC, *flags, *extra, "-c", os.path.join(CSRC, src), "-o", o], check=True,
                        stderr=subprocess.DEVNULL)

@@ -253,16 +253,40 @@ def test_f32_noise_envelope_bounds_the_oracle(kind, seed):
 def test_oracle_misses_the_flat_bar_only_on_near_guard_elements(kind, seed):
     """Where the f32 oracle itself is outside 1e-4 / 1e-3 of float64, the
     element's mel energy is at most 1e-6 of its frame's energy (f32 FFT
-    noise by construction); those are exactly the elements the GPU parity
-    check may widen, and the envelope there never exceeds its 5e-3 cap."""
+    noise by construction), or its row holds such elements and the miss is
+    within the row term (their noise moves the row's mean and std); those
+    are exactly the elements the GPU parity check may widen, and neither
+    term exceeds its 5e-3 cap."""
     from scriptrs_amd import synth
     a = synth.sinusoids(160_000, seed) if kind == "sin" else synth.speech_like(240_000, seed)[:238_080]
     r = R.extract(a)
     o = oracle.extract(a)
     near = R.near_guard(a)
-    env = R.f32_noise_envelope(a)
-    outside = np.abs(o - r) > 1e-4 + 1e-3 * np.abs(r)
-    assert not (outside & ~near).any()
-    assert np.all(env[~near] == 0.0) and env.max() <= R.ENV_CAP
-    print(f"{kind} {seed}: {int(outside.sum())} oracle elements outside the flat bar, all near-guard "
+    elem, row = R.f32_noise_envelope(a, parts=True)
+    excess = np.abs(o - r) - (1e-4 + 1e-3 * np.abs(r))
+    outside = excess > 0
+    assert not (outside & ~near & (excess > row)).any()
+    assert np.all(elem[~near] == 0.0) and elem.max() <= R.ENV_CAP and row.max() <= R.ENV_CAP
+    # the row term lives only in rows that hold near-guard elements
+    assert np.all(row[~near.any(axis=1)] == 0.0)
+    print(f"{kind} {seed}: {int(outside.sum())} oracle elements outside the flat bar, "
+          f"{int((outside & ~near).sum())} of them in rows of near-guard elements "
           f"({int(near.sum())} near-guard elements)")
+
+
+def test_row_term_covers_digital_silence_in_quiet_rows():
+    """A mostly quiet chunk with digitally silent frames (a task of the
+    synthetic speech recording of seed 707): silent frames are exact in
+    every implementation before normalisation, yet the oracle misses the
+    flat bar there, because the row's mean and std include near-guard
+    elements.  The row term covers every such miss."""
+    from scriptrs_amd import synth
+    a = synth.speech_like(3_000_000, 707)[2_262_720:2_368_540]
+    r = R.extract(a)
+    o = oracle.extract(a)
+    near = R.near_guard(a)
+    elem, row = R.f32_noise_envelope(a, parts=True)
+    excess = np.abs(o - r) - (1e-4 + 1e-3 * np.abs(r))
+    off_near = (excess > 0) & ~near
+    assert off_near.sum() > 100  # the case the row term exists for
+    assert np.all(excess[off_near] <= row[off_near])
