@@ -109,6 +109,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-other-configs", dest="other_configs", action="store_false",
                     help="config3 only: skip the short runs of configs 1, 2 and 4 reported beside it")
+    ap.add_argument("--no-config5", dest="config5", action="store_false",
+                    help="config3 only: leave config 5 (8 h streamed, about 40 s with its synthesis) out of "
+                         "the other configs")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed runs of each CPU baseline leg")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB per step (calibrates the HBM byte counters)")
@@ -309,7 +312,8 @@ def main() -> int:
 def other_configs(ext, args, steps: int = 50, warmup: int = 50) -> dict:
     """Wall-clock ms per step of configs 1, 2 and 4 (resident, f32), run
     after the headline workload in the same process: one launch sequence per
-    step, timed over `steps` steps after `warmup` untimed ones."""
+    step, timed over `steps` steps after `warmup` untimed ones; and config 5
+    (streamed) unless --no-config5."""
     import torch
     from scriptrs_amd import TaskTable
     res = {}
@@ -328,6 +332,22 @@ def other_configs(ext, args, steps: int = 50, warmup: int = 50) -> dict:
         torch.cuda.synchronize()
         res[name] = (time.perf_counter() - t0) / steps * 1e3
         del dev, out
+    if args.config5:
+        # Config 5: the 8 h recording streamed from pinned host memory in 60 s
+        # windows (PCIe-bound, 33 ms per step): 1 warmup and 3 timed steps.
+        x, tasks, _ = make_workload("config5")
+        tt = TaskTable(tasks)
+        host = torch.from_numpy(x).pin_memory().numpy()
+        del x
+        out = torch.empty(int(tt.frame_offsets[-1]) * 128, dtype=torch.float32, device="cuda")
+        ext.extract_chunks_streamed(host, tt, window_samples=960_000, out=out)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            ext.extract_chunks_streamed(host, tt, window_samples=960_000, out=out)
+        torch.cuda.synchronize()
+        res["config5"] = (time.perf_counter() - t0) / 3 * 1e3
+        del host, out
     return res
 
 
