@@ -251,11 +251,13 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
 
 /* Shared frames: on by default.  Overlapping chunk tasks of one call
  * (sfe_extract_chunks, _pcm, _padded, sfe_extract_batch) whose starts agree
- * modulo the hop have identical log-mel for the frames that lie inside both
- * (at least one sample inside each task's ends); those are computed once
- * and each task keeps its first and last 4-frame groups.  The output is
- * bitwise the same either way; turning it off makes every task compute all
- * of its frames (the streamed and allocation-free entry points always do). */
+ * modulo the hop have identical log-mel for a frame whose 512 padded
+ * samples lie, in every task that holds it, after the task's first sample
+ * and before its end; such frames are computed once and each task keeps
+ * its first and last 4-frame groups.  The output is bitwise the same either
+ * way; turning it off makes every task compute all of its frames (the
+ * streamed and allocation-free entry points always do).  Returns
+ * SFE_INVALID_ARG for a null ctx. */
 int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
 
 /* Turn per-kernel timing on or off for ctx.  When on, every launch of the

@@ -325,3 +325,9 @@ def test_max_feature_frames_null_and_zero_hop():
     L.sfe_config_default(ctypes.byref(c))
     c.hop_length = 0
     assert L.sfe_max_feature_frames(ctypes.byref(c)) == 240_000 // 160 + 1
+
+
+def test_tuning_calls_reject_null_context():
+    L = _lib.lib()
+    assert L.sfe_set_frame_sharing(None, 1) == _lib.SFE_INVALID_ARG
+    assert L.sfe_set_timing(None, 1) == _lib.SFE_INVALID_ARG
