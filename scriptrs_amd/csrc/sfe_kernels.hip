@@ -902,6 +902,21 @@ __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const flo
   norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, blockIdx.x, pad_to, out);
 }
 
+// Calls of few items (a clip, a small batch) leave most CUs idle with 4-wave
+// workgroups, and each workgroup's loads, reductions and stores run one
+// after another: 8-wave workgroups (128 frames per round, 33 KB of LDS for
+// the 512-frame transpose chunks) put twice the waves on each slab.
+constexpr int kNormWideWaves = 8;
+constexpr int kNormWideMaxItems = 16;
+
+template <int N, typename O>
+__global__ __launch_bounds__(64 * kNormWideWaves) void sfe_norm_wide_kernel(const float* __restrict__ raw,
+                                                                            const Item* __restrict__ items,
+                                                                            int n_items, int pad_to,
+                                                                            O* __restrict__ out) {
+  norm_body<kNormWideWaves, kNormMainSlab, N>(raw, items, n_items, blockIdx.x, pad_to, out);
+}
+
 }  // namespace
 
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
@@ -933,6 +948,13 @@ hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int m
                          hipStream_t stream) {
   using S = NormShape<kNormMainWaves, kNormMainSlab>;
   const unsigned blocks = (unsigned)((int64_t)n_items * S::kSlabs);
+  using SW = NormShape<kNormWideWaves, kNormMainSlab>;
+  if (n_items <= kNormWideMaxItems && max_T <= SW::kSpan * 16) {
+    const dim3 grid(blocks), block(SW::kThreads);
+    if (max_T <= SW::kSpan * 8) sfe_norm_wide_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+    else sfe_norm_wide_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+    return hipGetLastError();
+  }
   const dim3 grid(blocks), block(S::kThreads);
   // Registers per lane sized to the longest item (N float4s hold kSpan N
   // frames); longer items take the streaming path.
