@@ -226,6 +226,31 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   const int l = lane & 15;
   const int partner = (16 - l) & 15;
 
+  // Work: workgroup b owns units [wb, we) of this launch's [unit0, unit0 +
+  // n_units) (items[].unit_off counts in the same numbering), and its waves
+  // take them one at a time through an LDS counter, so a wave that gets less
+  // issue on its SIMD takes fewer units.  The persistent grid is 3
+  // workgroups per CU, dispatched a CU slot at a time; a SIMD issues its
+  // oldest wave first, so the later slots run slower, and with equal shares
+  // they finished 20 us after the first (1 h workload).  Shares are weighted
+  // 11 : 10 : 9 by slot (blocks in thirds of the grid) when every wave has
+  // at least 8 units.
+  __shared__ int wg_next;
+  int wb, we;
+  {
+    const int64_t G = gridDim.x, b = blockIdx.x, B1 = G / 3, B2 = 2 * G / 3;
+    const bool weighted = G >= 3 && (int64_t)n_units >= 8 * kWaves * G;
+    auto cum = [=](int64_t c) -> int64_t {  // share of the blocks before block c
+      if (!weighted) return c;
+      const int64_t c1 = c < B1 ? c : B1, c2 = c < B1 ? 0 : (c < B2 ? c - B1 : B2 - B1), c3 = c > B2 ? c - B2 : 0;
+      return 11 * c1 + 10 * c2 + 9 * c3;
+    };
+    const int64_t tot = cum(G);
+    wb = unit0 + (int)((int64_t)n_units * cum(b) / tot);
+    we = unit0 + (int)((int64_t)n_units * cum(b + 1) / tot);
+  }
+  if (tid == 0) wg_next = wb + kWaves;  // each wave's first unit is wb + w
+
   // A operands of the mel MFMAs, shared by the workgroup's waves.
   for (int i = tid; i < kMelVec * 64; i += kThreads) mel_a[i / 64][i % 64] = tb->mel_a[i / 64][i % 64];
   __syncthreads();
@@ -267,16 +292,12 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   // slab mj / 4 (chain 0; chain 1 is 4 slabs on), 4 features at 4 (mj % 4).
   const int so = 16 * mn + 256 * (mj >> 2) + 4 * (mj & 3);
 
-  // Persistent grid: each wave walks one contiguous range of units (quads
-  // of one item), so the per-lane constants above are loaded once per wave
-  // and neighbouring units, which share input lines, stay in one cache.
-  // Units of this launch are [unit0, unit0 + n_units) (items[].unit_off
-  // counts in the same numbering).
-  const int64_t nw = (int64_t)gridDim.x * kWaves;
-  const int64_t gw = (int64_t)blockIdx.x * kWaves + w;
-  const int u_begin = unit0 + (int)((int64_t)n_units * gw / nw);
-  const int u_end = unit0 + (int)((int64_t)n_units * (gw + 1) / nw);
-  if (u_begin >= u_end) return;
+  const int u_first = wb + w;
+  if (u_first >= we) return;
+  // The unit after the one being prefetched is taken one iteration ahead
+  // (lane 0's LDS add), so its result is in by the time it is needed.
+  int grab = 0;
+  if (lane == 0) grab = atomicAdd(&wg_next, 1);
   // Item descriptors stay in scalar registers: it_c is the item of the unit
   // being prefetched, it_n the item after it, loaded one item ahead so an
   // item boundary never waits on memory.  Every item spans at least one unit.
@@ -285,7 +306,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     int hi = n_items - 1;
     while (li < hi) {
       int mid = (li + hi + 1) >> 1;
-      if (items[mid].unit_off <= u_begin) li = mid;
+      if (items[mid].unit_off <= u_first) li = mid;
       else hi = mid - 1;
     }
   }
@@ -293,7 +314,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   Item it_n = items[li + 1 < n_items ? li + 1 : li];
   // The samples of unit u + 1 are loaded into registers while unit u is
   // transformed, so the global-load latency hides behind the FFT.
-  Span<S> sp_n = make_span(it_c, samples, u_begin);
+  Span<S> sp_n = make_span(it_c, samples, u_first);
   typename Pcm<S>::V4 nv[kSpanVec] = {};
   S nxm1 = 0;
   prefetch_span(sp_n, lane, nv, nxm1);
@@ -302,7 +323,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   // Raw offset (uniform) of the quad whose log-mel is held in acc0/acc1, or -1.
   int64_t pend = -1;
 
-  for (int u = u_begin; u < u_end; ++u) {
+  for (int u = u_first, un; u < we; u = un) {
     const Item it = it_c;
     const Span<S> sp = sp_n;
     // (for a span that is not interior nv holds stale values, decoded and
@@ -369,13 +390,16 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     // Then the next unit's samples are requested.  Vector memory operations
     // complete in issue order, so loading after the stores means the wait
     // for these samples, a quad from now, never waits on fresh stores.
-    if (u + 1 < u_end) {
-      if (li + 1 < n_items && u + 1 >= it_n.unit_off) {
+    un = __builtin_amdgcn_readfirstlane(grab);
+    if (un < we) {
+      if (lane == 0) grab = atomicAdd(&wg_next, 1);
+      // (units only increase: the items are walked forward)
+      while (li + 1 < n_items && un >= it_n.unit_off) {
         ++li;
         it_c = it_n;
         it_n = items[li + 1 < n_items ? li + 1 : li];
       }
-      sp_n = make_span(it_c, samples, u + 1);
+      sp_n = make_span(it_c, samples, un);
       prefetch_span(sp_n, lane, nv, nxm1);
     }
     wave_lds_sync();
