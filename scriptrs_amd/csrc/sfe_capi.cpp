@@ -167,7 +167,7 @@ bool shape_supported(const sfe_config* c, std::string* why) {
 struct sfe_ctx {
   sfe_config cfg;
   int device = 0;
-  int grid_cap = 512;  // resident log-mel workgroups: CUs x blocks per CU
+  int cus = 256;  // compute units of the device
   std::mutex mu;
   sfe::DevTables* d_tables = nullptr;
   hipStream_t s_compute = nullptr;  // internal streams, default priority
@@ -290,7 +290,7 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* lm, const Item* d_l
   if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
   if (stages & kLogmel)
     SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_lm, n_lm, u0, u1 - u0, ctx->d_tables,
-                               ctx->cfg.preemphasis, raw, ctx->grid_cap, stream));
+                               ctx->cfg.preemphasis, raw, ctx->cus, stream));
   if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
   if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
   if (stages & kNorm)
@@ -504,7 +504,7 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
     ctx->device = device;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
-      ctx->grid_cap = cus * sfe::kLogmelBlocksPerCU;
+      ctx->cus = cus;
     auto cleanup = [&](int rc) {
       sfe_destroy(ctx);
       return rc;

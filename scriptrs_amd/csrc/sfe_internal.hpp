@@ -125,19 +125,17 @@ bool build_dev_tables(int sample_rate, DevTables* t);
 // Kernel launchers (sfe_kernels.hip).  All asynchronous on `stream`.
 int64_t tiles_for(int64_t T);
 int64_t units_for(int64_t T);  // quads of an item: ceil(T / 4)
-// grid_cap: workgroups resident on the device at once (the kernel loops
-// over tiles, so launching more than that only adds scheduling overhead).
-// Input sample formats: f32, or integer PCM (16-bit or 32-bit containers)
+// cus: the device's compute units (the log-mel grid is persistent: at most
+// the workgroups resident at once).  Input sample formats: f32, or integer PCM (16-bit or 32-bit containers)
 // decoded as value / pcm_scale in the kernel.
 constexpr int kPcmF32 = 0;
 constexpr int kPcmI16 = 1;
 constexpr int kPcmI32 = 2;
 // Units [unit0, unit0 + n_units) in the numbering of items[].unit_off.
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
-                         int n_units, const DevTables* tables, float preemph, float* raw_out, int grid_cap,
+                         int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
                          hipStream_t stream);
 constexpr int kLogmelWavesPerSimd = 3;
-constexpr int kLogmelBlocksPerCU = kLogmelWavesPerSimd;  // 4-wave workgroups: one wave per SIMD each
 // Normalises raw (f32 log2 values in 16-frame tiles, see Item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's

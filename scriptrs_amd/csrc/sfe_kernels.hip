@@ -1,6 +1,6 @@
 // CDNA4 (gfx950) kernels of the log-mel front end.
 //
-// sfe_logmel_kernel fuses, per pass of 16 frames of one item, everything
+// sfe_logmel_kernel fuses, per quad of 4 frames of one item, everything
 // ParakeetFeatureExtractor::extract does before normalisation
 // (src/frontend.rs:104-147, :150-159):
 //   preemphasis restarted at the item start -> 256-zero padding ->
@@ -30,8 +30,11 @@
 namespace sfe {
 namespace {
 
-constexpr int kWaves = 4;               // log-mel workgroup: independent waves
-constexpr int kThreads = 64 * kWaves;
+// Log-mel workgroups hold independent waves: 4 (three workgroups per CU)
+// for launches that do not fill the machine, 12 (one per CU, all of its
+// waves sharing one work counter) for those that do.
+constexpr int kWavesSmall = 4;
+constexpr int kWavesBig = 12;
 constexpr int kXStride = 17;                         // transpose row stride (complex)
 constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
 constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
@@ -212,10 +215,12 @@ __device__ __forceinline__ void mfma_keep(const float4& a, const float4& b) {
   asm volatile("" ::"v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(b.x), "v"(b.y), "v"(b.z), "v"(b.w));
 }
 
-template <typename S>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kLogmelWavesPerSimd, kLogmelWavesPerSimd)))
+template <typename S, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kLogmelWavesPerSimd, kLogmelWavesPerSimd)))
 void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ items, int n_items, int unit0,
                        int n_units, const DevTables* __restrict__ tb, float coef, Decode dc, float* __restrict__ out) {
+  constexpr int kWaves = NW;
+  constexpr int kThreads = 64 * NW;
   __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
   __shared__ __align__(16) float4 mel_a[kMelVec][64];
 
@@ -229,17 +234,17 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   // Work: workgroup b owns units [wb, we) of this launch's [unit0, unit0 +
   // n_units) (items[].unit_off counts in the same numbering), and its waves
   // take them one at a time through an LDS counter, so a wave that gets less
-  // issue on its SIMD takes fewer units.  The persistent grid is 3
-  // workgroups per CU, dispatched a CU slot at a time; a SIMD issues its
-  // oldest wave first, so the later slots run slower, and with equal shares
-  // they finished 20 us after the first (1 h workload).  Shares are weighted
-  // 11 : 10 : 9 by slot (blocks in thirds of the grid) when every wave has
-  // at least 8 units.
+  // issue on its SIMD takes fewer units.  With 4-wave workgroups the
+  // persistent grid is 3 workgroups per CU, dispatched a CU slot at a time;
+  // a SIMD issues its oldest wave first, so the later slots run slower, and
+  // with equal shares they finished 20 us after the first (1 h workload).
+  // Their shares are then weighted 11 : 10 : 9 by slot (blocks in thirds of
+  // the grid) when every wave has at least 8 units.
   __shared__ int wg_next;
   int wb, we;
   {
     const int64_t G = gridDim.x, b = blockIdx.x, B1 = G / 3, B2 = 2 * G / 3;
-    const bool weighted = G >= 3 && (int64_t)n_units >= 8 * kWaves * G;
+    const bool weighted = NW == kWavesSmall && G >= 3 && (int64_t)n_units >= 8 * kWaves * G;
     auto cum = [=](int64_t c) -> int64_t {  // share of the blocks before block c
       if (!weighted) return c;
       const int64_t c1 = c < B1 ? c : B1, c2 = c < B1 ? 0 : (c < B2 ? c - B1 : B2 - B1), c3 = c > B2 ? c - B2 : 0;
@@ -946,25 +951,41 @@ __global__ __launch_bounds__(64 * kNormWideWaves) void sfe_norm_wide_kernel(cons
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
 int64_t units_for(int64_t T) { return (T + kQuad - 1) / kQuad; }
 
+template <int NW>
+hipError_t launch_logmel_t(const void* samples, int pcm, const Decode& dc, const Item* items, int n_items, int unit0,
+                           int n_units, const DevTables* tables, float preemph, float* raw_out, int grid,
+                           hipStream_t stream) {
+  const dim3 g(grid), b(64 * NW);
+  if (pcm == kPcmI16)
+    sfe_logmel_kernel<int16_t, NW><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items, unit0,
+                                                        n_units, tables, preemph, dc, raw_out);
+  else if (pcm == kPcmI32)
+    sfe_logmel_kernel<int32_t, NW><<<g, b, 0, stream>>>(static_cast<const int32_t*>(samples), items, n_items, unit0,
+                                                        n_units, tables, preemph, dc, raw_out);
+  else
+    sfe_logmel_kernel<float, NW><<<g, b, 0, stream>>>(static_cast<const float*>(samples), items, n_items, unit0,
+                                                      n_units, tables, preemph, dc, raw_out);
+  return hipGetLastError();
+}
+
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
-                         int n_units, const DevTables* tables, float preemph, float* raw_out, int grid_cap,
+                         int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
                          hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
-  // Each wave takes at least one unit; at most grid_cap workgroups are resident.
-  const int want = (n_units + kWaves - 1) / kWaves;
-  const int grid = want < grid_cap ? want : grid_cap;
   Decode dc{pcm_scale, 1.0f / pcm_scale, 1.0 / (double)pcm_scale};  // the host's divisions are correctly rounded
-  const dim3 g(grid), b(kThreads);
-  if (pcm == kPcmI16)
-    sfe_logmel_kernel<int16_t><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items, unit0,
-                                                    n_units, tables, preemph, dc, raw_out);
-  else if (pcm == kPcmI32)
-    sfe_logmel_kernel<int32_t><<<g, b, 0, stream>>>(static_cast<const int32_t*>(samples), items, n_items, unit0,
-                                                    n_units, tables, preemph, dc, raw_out);
-  else
-    sfe_logmel_kernel<float><<<g, b, 0, stream>>>(static_cast<const float*>(samples), items, n_items, unit0, n_units,
-                                                  tables, preemph, dc, raw_out);
-  return hipGetLastError();
+  // A launch with at least 4 units per wave on every CU's 12 waves takes one
+  // 12-wave workgroup per CU; smaller ones 4-wave workgroups, up to 3 per CU,
+  // each wave taking at least one unit (one per wave when they do not fill
+  // the machine, which spreads a small launch over more CUs).
+  if ((int64_t)n_units >= (int64_t)4 * kWavesBig * cus) {
+    const int want = (n_units + kWavesBig - 1) / kWavesBig;
+    return launch_logmel_t<kWavesBig>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out,
+                                      want < cus ? want : cus, stream);
+  }
+  const int want = (n_units + kWavesSmall - 1) / kWavesSmall;
+  const int cap = kLogmelWavesPerSimd * cus;
+  return launch_logmel_t<kWavesSmall>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out,
+                                      want < cap ? want : cap, stream);
 }
 
 template <typename O>
