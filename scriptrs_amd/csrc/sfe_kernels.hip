@@ -124,8 +124,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Work of one wave: a contiguous range of units; a unit (a quad) is 4
-// consecutive frames of one item.  Waves are independent: each owns an LDS
+// Work of one wave: units taken one at a time from its workgroup's range; a
+// unit (a quad) is 4 consecutive frames of one item.  Waves are independent
+// but for that counter: each owns an LDS
 // region in which its quad's samples, FFT transpose and power spectra live
 // in turn, and contracts its own 4 frames with all 128 filters on the matrix
 // cores (v_mfma_f32_4x4x1_16b_f32).  The only workgroup barrier is the one
