@@ -318,6 +318,11 @@ int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, i
     std::vector<Item> lm, norm;
     ctx->plan_tiles = sfe::plan_items(items.data(), (int)items.size(), ctx->share, &lm, &norm);
     ctx->plan_n_lm = lm.size();
+    // Normalisation workgroups start in table order: longest items first (in
+    // classes of 256 frames, call order within one), so the last ones to
+    // start are short; each entry writes its own dst_off, so the order is
+    // free.  Ragged batches (config 4): 0.0738 -> 0.0713 ms.
+    std::stable_sort(norm.begin(), norm.end(), [](const Item& a, const Item& b) { return (a.T >> 8) > (b.T >> 8); });
     lm.insert(lm.end(), norm.begin(), norm.end());
     ctx->plan_table.swap(lm);
     ctx->plan_in = items;
