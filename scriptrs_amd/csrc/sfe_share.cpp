@@ -105,11 +105,12 @@ int64_t plan_items(const Item* items, int n, bool share, std::vector<Item>* lm, 
   }
 
   // Raw regions, in item order (a run's shared region and its members' own
-  // tiles where its first member is), and log-mel entries.  The shared entry is cut at its
-  // members' starts, and all entries are then ordered by the recording
-  // position of their first frame: the first and last quads of items, whose
-  // samples cross an item's ends and take the kernel's slower per-sample
-  // path, are spread over the launch instead of falling to a few waves.
+  // tiles where its first member is), and log-mel entries.  The shared
+  // entry is cut at its members' starts, and all entries are then ordered by
+  // the recording position of their first frame: the first and last quads
+  // of items, whose samples cross an item's ends and take the kernel's
+  // slower per-sample path, are spread over the launch instead of falling
+  // to a few waves.
   int64_t tiles = 0;
   std::vector<std::pair<int64_t, Item>> pieces;  // (position, entry)
   std::vector<int64_t> run_grid(runs.size(), -1);  // grid_off of each run
