@@ -312,8 +312,9 @@ def main() -> int:
 def other_configs(ext, args, steps: int = 50, warmup: int = 50) -> dict:
     """Wall-clock ms per step of configs 1, 2 and 4 (resident, f32), run
     after the headline workload in the same process: one launch sequence per
-    step, timed over `steps` steps after `warmup` untimed ones; and config 5
-    (streamed) unless --no-config5."""
+    step, timed over `steps` steps after at least `warmup` untimed ones
+    (and at least 100 ms of them); and config 5 (streamed) unless
+    --no-config5."""
     import torch
     from scriptrs_amd import TaskTable
     res = {}
@@ -323,9 +324,16 @@ def other_configs(ext, args, steps: int = 50, warmup: int = 50) -> dict:
         tt = TaskTable(tasks)
         dev = torch.from_numpy(x).cuda()
         out = torch.empty(int(tt.frame_offsets[-1]) * 128, dtype=torch.float32, device="cuda")
-        for _ in range(warmup):
-            ext.extract_chunks(dev, tt, stream=stream, out=out)
-        torch.cuda.synchronize()
+        # At least `warmup` steps and 100 ms of them: the GPU idled while the
+        # workload was synthesized, and its clock ramps back up over tens of
+        # milliseconds of load.
+        tw = time.perf_counter()
+        done = 0
+        while done < warmup or time.perf_counter() - tw < 0.1:
+            for _ in range(warmup):
+                ext.extract_chunks(dev, tt, stream=stream, out=out)
+            torch.cuda.synchronize()
+            done += warmup
         t0 = time.perf_counter()
         for _ in range(steps):
             ext.extract_chunks(dev, tt, stream=stream, out=out)
