@@ -71,6 +71,24 @@ def measured_traffic(fname: str, applies: bool):
     return measured_profile(fname, applies)
 
 
+def warm_up(step, steps: int, min_s: float) -> None:
+    """At least `steps` untimed steps and `min_s` seconds of them (unless
+    steps is 0), for the extra configs reported beside the headline (whose
+    warmup is exactly --warmup steps): the GPU idles while a workload is
+    synthesized, and its clock ramps back up over tens of milliseconds of
+    load."""
+    import torch
+    if steps <= 0:
+        return
+    t0 = time.perf_counter()
+    done = 0
+    while done < steps or time.perf_counter() - t0 < min_s:
+        for _ in range(steps - done if done < steps else max(1, steps // 4)):
+            step()
+            done += 1
+        torch.cuda.synchronize()
+
+
 def make_workload(name: str):
     from scriptrs_amd import synth
     from scriptrs_amd.long_form import build_fast_execution_plan, ChunkTask
@@ -324,16 +342,7 @@ def other_configs(ext, args, steps: int = 50, warmup: int = 50) -> dict:
         tt = TaskTable(tasks)
         dev = torch.from_numpy(x).cuda()
         out = torch.empty(int(tt.frame_offsets[-1]) * 128, dtype=torch.float32, device="cuda")
-        # At least `warmup` steps and 100 ms of them: the GPU idled while the
-        # workload was synthesized, and its clock ramps back up over tens of
-        # milliseconds of load.
-        tw = time.perf_counter()
-        done = 0
-        while done < warmup or time.perf_counter() - tw < 0.1:
-            for _ in range(warmup):
-                ext.extract_chunks(dev, tt, stream=stream, out=out)
-            torch.cuda.synchronize()
-            done += warmup
+        warm_up(lambda: ext.extract_chunks(dev, tt, stream=stream, out=out), warmup, 0.1)
         t0 = time.perf_counter()
         for _ in range(steps):
             ext.extract_chunks(dev, tt, stream=stream, out=out)
