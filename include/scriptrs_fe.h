@@ -192,7 +192,8 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It runs the same kernels as sfe_extract_chunks, with the same
- * results, but keeps its item table and raw log-mel in a static device array
+ * results (frames that tasks share computed once, as there), but keeps its
+ * item table and raw log-mel in a static device array
  * of the library (one per GPU, held until the process ends) instead of the
  * context's growable buffers, and calls no hipMalloc, hipFree or other
  * allocating routine.  Limits: at most 4096 tasks, and at most 64 MiB of raw
@@ -256,7 +257,8 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
  * and before its end; such frames are computed once and each task keeps
  * its first and last 4-frame groups.  The output is bitwise the same either
  * way; turning it off makes every task compute all of its frames (the
- * streamed and allocation-free entry points always do).  Returns
+ * streamed entry points always do).  sfe_extract_chunks_noalloc follows
+ * the setting too.  Returns
  * SFE_INVALID_ARG for a null ctx. */
 int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
 

@@ -208,6 +208,10 @@ struct sfe_ctx {
   // then raw log-mel.  Looked up at creation; h_meta is reserved for its
   // largest item table at creation too.
   unsigned char* noalloc = nullptr;
+  // Host staging of its planner, also reserved at creation for
+  // kNoAllocMaxItems items: the chunks' own items and the planner's lists.
+  std::vector<Item> na_in;
+  sfe::PlanWorkspace na_ws;
 };
 
 namespace {
@@ -315,16 +319,16 @@ int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, i
   // one table: the log-mel entries, then the normalisation entries
   if (!(ctx->plan_share == ctx->share && ctx->plan_in.size() == items.size() &&
         memcmp(ctx->plan_in.data(), items.data(), items.size() * sizeof(Item)) == 0)) {
-    std::vector<Item> lm, norm;
-    ctx->plan_tiles = sfe::plan_items(items.data(), (int)items.size(), ctx->share, &lm, &norm);
-    ctx->plan_n_lm = lm.size();
-    // Normalisation workgroups start in table order: longest items first (in
-    // classes of 256 frames, call order within one), so the last ones to
-    // start are short; each entry writes its own dst_off, so the order is
-    // free.  Ragged batches (config 4): 0.0738 -> 0.0713 ms.
-    std::stable_sort(norm.begin(), norm.end(), [](const Item& a, const Item& b) { return (a.T >> 8) > (b.T >> 8); });
-    lm.insert(lm.end(), norm.begin(), norm.end());
-    ctx->plan_table.swap(lm);
+    const int n = (int)items.size();
+    sfe::PlanWorkspace ws;
+    ws.reserve(items.size());
+    std::vector<Item> table((size_t)(sfe::kPlanEntriesPerItem + 1) * items.size());
+    size_t n_lm = 0;
+    ctx->plan_tiles = sfe::plan_table(items.data(), n, ctx->share, &ws, table.data(), &n_lm);
+    sfe::order_norm(table.data() + n_lm, n);
+    table.resize(n_lm + items.size());
+    ctx->plan_n_lm = n_lm;
+    ctx->plan_table.swap(table);
     ctx->plan_in = items;
     ctx->plan_share = ctx->share;
   }
@@ -526,8 +530,9 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
     void* na = nullptr;
     if ((e = sfe::noalloc_scratch(device, &na)) != hipSuccess) return cleanup(hip_fail(e, "hipGetSymbolAddress(scratch)"));
     ctx->noalloc = static_cast<unsigned char*>(na);
-    if ((e = ctx->h_meta.reserve((size_t)sfe::kNoAllocMaxItems * sizeof(Item))) != hipSuccess)
-      return cleanup(hip_fail(e, "hipHostMalloc"));
+    if ((e = ctx->h_meta.reserve(sfe::kNoAllocItemBytes)) != hipSuccess) return cleanup(hip_fail(e, "hipHostMalloc"));
+    ctx->na_in.reserve(sfe::kNoAllocMaxItems);
+    ctx->na_ws.reserve(sfe::kNoAllocMaxItems);
     for (int i = 0; i < 2; ++i) {
       if ((e = hipEventCreateWithFlags(&ctx->ev_copied[i], hipEventDisableTiming)) != hipSuccess)
         return cleanup(hip_fail(e, "hipEventCreate"));
@@ -704,8 +709,10 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
                                int32_t n, int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream) {
   // sfe_extract_chunks with the item table and the raw log-mel in this
   // device's static scratch: no device or host allocation on any path that
-  // succeeds (the item table is built in the context's pinned buffer, which
-  // sfe_create reserved for kNoAllocMaxItems items).
+  // succeeds.  The plan (frames shared as in sfe_extract_chunks) is built in
+  // host buffers that sfe_create reserved for kNoAllocMaxItems items: the
+  // planner's lists stay within that capacity and std::sort allocates
+  // nothing.
   return guarded([&]() -> int {
     if (n <= 0 || !tasks || !recording || !out || !frame_offsets) return fail(SFE_INVALID_ARG, "invalid chunk arguments");
     if (n > sfe::kNoAllocMaxItems)
@@ -713,7 +720,7 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
                                        " tasks");
     int rc = check_dtype(out_dtype);
     if (rc) return rc;
-    int64_t tiles = 0, fo = 0;
+    int64_t tiles = 0;
     for (int32_t i = 0; i < n; ++i) {
       const sfe_chunk& t = tasks[i];
       if (t.audio_start < 0 || t.audio_end > len || t.audio_end < t.audio_start)
@@ -722,37 +729,46 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
       if (L == 0) return fail(SFE_EMPTY_AUDIO, "audio input was empty (item " + std::to_string(i) + ")");
       tiles += sfe::tiles_for(L / sfe::kHop + 1);
     }
+    // The limit is on the tasks' own regions: a plan with shared frames that
+    // would need more tiles than that (tile rounding of the items' first and
+    // last quads) is replaced by the plan without sharing.
     const size_t raw_bytes = (size_t)tiles * sfe::kRawTile * sizeof(float);
     if (raw_bytes > sfe::kNoAllocRawBytes)
       return fail(SFE_INVALID_ARG, "sfe_extract_chunks_noalloc: the tasks need " + std::to_string(raw_bytes) +
                                        " bytes of scratch, more than its " + std::to_string(sfe::kNoAllocRawBytes));
     if ((rc = check_ctx(ctx))) return rc;
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (!ctx->noalloc || ctx->h_meta.cap < (size_t)n * sizeof(Item))
+    const size_t entries = (size_t)(sfe::kPlanEntriesPerItem + 1) * n;
+    if (!ctx->noalloc || ctx->h_meta.cap < entries * sizeof(Item) || ctx->na_in.capacity() < (size_t)n)
       return fail(SFE_HIP_ERROR, "context has no static scratch");
-    // The pinned table is free once its previous upload has finished.
-    SFE_HIP(ctx->h_meta.wait());
-    Item* items = static_cast<Item*>(ctx->h_meta.ptr);
-    tiles = 0;
-    int64_t units = 0;
+    int64_t fo = 0, own_tiles = 0;
     frame_offsets[0] = 0;
+    ctx->na_in.clear();
     for (int32_t i = 0; i < n; ++i) {
-      Item& it = items[i];
-      it = sfe::own_item(tasks[i].audio_start, tasks[i].audio_end - tasks[i].audio_start, (int64_t)sfe::kRawTile * tiles,
-                         (int64_t)sfe::kMel * fo, (int32_t)units);
+      const Item it = sfe::own_item(tasks[i].audio_start, tasks[i].audio_end - tasks[i].audio_start, 0,
+                                    (int64_t)sfe::kMel * fo, 0);
+      ctx->na_in.push_back(it);
       fo += it.T;
-      tiles += sfe::tiles_for(it.T);
-      units += sfe::units_for(it.T);
+      own_tiles += sfe::tiles_for(it.T);
       frame_offsets[i + 1] = fo;
     }
+    // The pinned table is free once its previous upload has finished.
+    SFE_HIP(ctx->h_meta.wait());
+    Item* table = static_cast<Item*>(ctx->h_meta.ptr);
+    size_t n_lm = 0;
+    bool share = ctx->share;
+    tiles = sfe::plan_table(ctx->na_in.data(), n, share, &ctx->na_ws, table, &n_lm);
+    if (share && tiles > own_tiles) tiles = sfe::plan_table(ctx->na_in.data(), n, false, &ctx->na_ws, table, &n_lm);
+    sfe::order_norm(table + n_lm, n);
     hipStream_t s = static_cast<hipStream_t>(stream);
     SFE_HIP(order_after_last(ctx, s));
-    Item* d_items = reinterpret_cast<Item*>(ctx->noalloc);
+    Item* d_table = reinterpret_cast<Item*>(ctx->noalloc);
     float* raw = reinterpret_cast<float*>(ctx->noalloc + sfe::kNoAllocItemBytes);
-    SFE_HIP(hipMemcpyAsync(d_items, items, (size_t)n * sizeof(Item), hipMemcpyHostToDevice, s));
+    SFE_HIP(hipMemcpyAsync(d_table, table, (n_lm + n) * sizeof(Item), hipMemcpyHostToDevice, s));
     SFE_HIP(hipEventRecord(ctx->h_meta.ev, s));
     ctx->h_meta.pending = true;
-    rc = launch_own(ctx, f32_source(recording), items, d_items, n, raw, out, out_dtype, 0, s, kBoth, false);
+    rc = launch_pair(ctx, f32_source(recording), table, d_table, (int)n_lm, table + n_lm, d_table + n_lm, n, raw, out,
+                     out_dtype, 0, s, kBoth, false);
     if (rc) return rc;
     SFE_HIP(mark_last(ctx, s));
     return SFE_OK;

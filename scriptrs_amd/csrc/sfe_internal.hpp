@@ -99,6 +99,38 @@ inline Item own_item(int64_t start, int64_t len, int64_t out_off, int64_t dst_of
 // and returns the raw tiles they use.  With share = false, or where sharing
 // saves no quads, every item keeps its own region.
 int64_t plan_items(const Item* items, int n, bool share, std::vector<Item>* lm, std::vector<Item>* norm);
+// The same into one table without allocating: table[0, *n_lm) gets the
+// log-mel entries, table[*n_lm, *n_lm + n) the normalisation entries in item
+// order.  table holds (kPlanEntriesPerItem + 1) n entries; nothing is
+// allocated when ws was reserved for at least n items.
+constexpr int kPlanEntriesPerItem = 3;  // log-mel entries per item at most
+struct PlanWorkspace {
+  struct Span {
+    int idx;              // item index
+    int64_t res, lo, hi;  // start mod hop; interior frames in recording frame indices
+  };
+  struct Run {
+    int64_t res, lo, hi;   // union of interior frames (recording frame indices)
+    int64_t vstart, vend;  // samples of the shared entry
+    int64_t cv;            // vstart / hop
+    int64_t grid;          // out_off of the shared entry once placed, else -1
+    int k0, k1;            // members: sp[k0, k1)
+  };
+  struct Piece {
+    int64_t pos;  // recording position of the first frame
+    int32_t seq;  // creation order
+    Item e;
+  };
+  std::vector<Span> sp;
+  std::vector<int> run_of;
+  std::vector<Run> runs;
+  std::vector<Piece> pieces;
+  void reserve(size_t n);
+};
+int64_t plan_table(const Item* items, int n, bool share, PlanWorkspace* ws, Item* table, size_t* n_lm);
+// Normalisation entries reordered longest first (in 256-frame classes, call
+// order within one); allocates nothing.
+void order_norm(Item* norm, int n);
 // Frames of one run's shared entry at most (512 MB of raw log-mel): an
 // item's first and last tiles follow its run's shared region, within 4 GB.
 constexpr int64_t kMaxShareFrames = (int64_t)1 << 20;
@@ -148,7 +180,10 @@ hipError_t launch_norm(const float* raw, const Item* items, int n_items, int max
 // item table of up to kNoAllocMaxItems items, then kNoAllocRawBytes of raw
 // log-mel (kNoAllocRawBytes / (kRawTile * 4) 16-frame tiles).
 constexpr int kNoAllocMaxItems = 4096;
-constexpr size_t kNoAllocItemBytes = ((size_t)kNoAllocMaxItems * sizeof(Item) + 255) / 256 * 256;
+// (a plan has at most kPlanEntriesPerItem log-mel entries and one
+// normalisation entry per item)
+constexpr size_t kNoAllocItemBytes =
+    ((size_t)(kPlanEntriesPerItem + 1) * kNoAllocMaxItems * sizeof(Item) + 255) / 256 * 256;
 constexpr size_t kNoAllocRawBytes = (size_t)64 << 20;
 // Device address of this device's static scratch (looked up once per device).
 hipError_t noalloc_scratch(int device, void** out);

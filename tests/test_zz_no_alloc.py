@@ -67,3 +67,33 @@ def test_noalloc_rejects_calls_past_its_limits(extractor):
     rc, _ = _noalloc(ctx, dev, many, out, _lib.SFE_F32, stream)
     assert rc == _lib.SFE_INVALID_ARG and "4096" in _lib.last_error()
     torch.cuda.synchronize()
+
+
+def test_noalloc_shared_plan_at_its_raw_limit(extractor):
+    """1024 heavily overlapping tasks (starts 5 hops apart, 126 frames each):
+    their own regions fill the 64 MiB raw array exactly, and with sharing on
+    the plan has about 3 log-mel entries per task.  Both plans must give
+    sfe_extract_chunks' output bit for bit."""
+    import torch
+    stream = torch.cuda.current_stream()
+    ctx = extractor._handle()
+    n_tasks, step, length = 1024, 800, 20_000
+    rec = synth.speech_like((n_tasks - 1) * step + length, 31)
+    tt = TaskTable(np.array([[i * step, i * step + length, i * step, 0] for i in range(n_tasks)], np.int64))
+    dev = torch.from_numpy(rec).cuda()
+    outs = []
+    try:
+        for share in (True, False):
+            _flush(f"case: noalloc 1024 overlapping tasks, sharing {share}")
+            extractor.set_frame_sharing(share)
+            want, wfo = extractor.extract_chunks(dev, tt, dtype="f32", stream=stream)
+            got = torch.full_like(want, float("nan"))
+            rc, fo = _noalloc(ctx, dev, tt, got, _lib.SFE_F32, stream)
+            assert rc == _lib.SFE_OK, _lib.last_error()
+            torch.cuda.synchronize()
+            assert np.array_equal(fo, wfo)
+            assert torch.equal(got, want), share
+            outs.append(got)
+    finally:
+        extractor.set_frame_sharing(True)
+    assert torch.equal(outs[0], outs[1])
