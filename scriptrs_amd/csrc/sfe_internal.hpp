@@ -131,9 +131,18 @@ int64_t plan_table(const Item* items, int n, bool share, PlanWorkspace* ws, Item
 // Normalisation entries reordered longest first (in 256-frame classes, call
 // order within one); allocates nothing.
 void order_norm(Item* norm, int n);
-// Frames of one run's shared entry at most (512 MB of raw log-mel): an
-// item's first and last tiles follow its run's shared region, within 4 GB.
+// Frames of one run's shared entry at most (512 MB of raw log-mel), and
+// members of one run at most (each with at most 3 tiles of its own, 384 MB
+// in all): an item's first and last tiles follow its run's shared region,
+// and every frame of the item lies within kNormBufRange bytes of the
+// region's start (the normalisation kernel's 32-bit buffer offsets).
 constexpr int64_t kMaxShareFrames = (int64_t)1 << 20;
+constexpr int kMaxShareMembers = 1 << 14;
+constexpr int kNormBufRange = 0x7ffffff0;
+static_assert(kMaxShareFrames * kRawTile / kTile * 4 + (int64_t)kMaxShareMembers * 3 * kRawTile * 4 +
+                      (int64_t)2 * kRawTile * 4 <
+                  kNormBufRange,
+              "a run's regions fit the normalisation kernel's offsets");
 
 // Constant tables, uploaded once per context.
 struct DevTables {

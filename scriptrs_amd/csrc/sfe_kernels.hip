@@ -571,6 +571,8 @@ __device__ __forceinline__ void constant_row_stats(float x0, int T, float* mean_
 // values are all equal replays the reference's sequential f32 sums
 // (constant_row_stats).
 constexpr int kNormBatch = 8;                  // rounds of loads in flight on the streaming path
+// Fourth word of a raw buffer resource (no format conversion, no swizzle).
+constexpr int kBufWord3 = 0x00020000;
 constexpr int kNormFlush = 8;                  // f32 partial sums span at most this many values
 
 // Shape of a normalisation workgroup: W waves, a slab of F features.
@@ -784,12 +786,13 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   const uint32_t dlo = 4u * (uint32_t)(it.out_off - it.grid_off + raw_frame(fr) - raw_frame(fr + it.gshift));
   const uint32_t dhi = 4u * (uint32_t)(it.tail_off - it.grid_off + raw_frame(fr) - raw_frame(fr + it.gshift));
   const int flo = f_lo - fr, fhi = f_hi - fr;  // round j holds frame fr + kSpan j
-  auto round = [og, dlo, dhi, flo, fhi, bg](int j) -> const float4* {
+  auto roff = [og, dlo, dhi, flo, fhi](int j) -> uint32_t {
     const int d = kSpan * j;
     uint32_t o = og + kRound * (uint32_t)j + (d > fhi ? dhi : 0u);
     if (j == 0) o += flo > 0 ? dlo : 0u;
-    return reinterpret_cast<const float4*>(bg + o);
+    return o;
   };
+  auto round = [roff, bg](int j) -> const float4* { return reinterpret_cast<const float4*>(bg + roff(j)); };
   const int rs = pad_to > 0 ? pad_to : T;  // output row length
   O* ob = out + it.dst_off + (size_t)slab * rs;
   if (pad_to > 0) zero_tail<W, F>(ob, T, rs, lane, w);
@@ -801,11 +804,17 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   if constexpr (N > 0) {
     if (T <= kSpan * N) {
       float4 v[N];
-      // Unconditional loads from an in-bounds frame (rounds past the item
-      // reread the lane's first frame), selected afterwards: a load under a
-      // branch waits for itself, and the rounds would load one at a time.
+      // Raw buffer loads from the uniform base, all issued before any is
+      // used (a load under a per-lane branch would wait for itself).  Rounds
+      // past the lane's frames take an offset past the buffer's range: the
+      // hardware returns zeros for them without a memory access, and the
+      // select below replaces them.
+      const __amdgpu_buffer_rsrc_t rsrc =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(bg), 0, kNormBufRange, kBufWord3);
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[j] = *(j < nr ? round(j) : (nr > 0 ? round(0) : p0));
+      for (int j = 0; j < N; ++j)
+        v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rsrc, (int)(j < nr ? roff(j) : kNormBufRange), 0, 0));
 #pragma unroll
       for (int j = 0; j < N; ++j) v[j] = j < nr ? ln2_scale(v[j]) : x0;  // x0 padding keeps the constancy test exact
 #pragma unroll

@@ -70,11 +70,11 @@ int64_t plan_table(const Item* items, int n, bool share, PlanWorkspace* ws, Item
     for (size_t k = 0; k < sp.size();) {
       const Item& f = items[sp[k].idx];
       PlanWorkspace::Run r{sp[k].res, sp[k].lo, sp[k].hi, f.start, f.start + f.len, 0, -1, (int)k, (int)k + 1};
-      // A run's shared frames stay within kMaxShareFrames: the normalisation
-      // kernel addresses an item's regions by 32-bit byte offsets from its
-      // shared region.
+      // A run's shared frames and members stay within kMaxShareFrames and
+      // kMaxShareMembers: the normalisation kernel addresses an item's
+      // regions by 32-bit byte offsets from its shared region.
       for (size_t m = k + 1; m < sp.size() && sp[m].res == r.res && sp[m].lo <= r.hi + 1 &&
-                             std::max(r.hi, sp[m].hi) - r.lo < kMaxShareFrames;
+                             std::max(r.hi, sp[m].hi) - r.lo < kMaxShareFrames && (int)m - r.k0 < kMaxShareMembers;
            ++m) {
         const Item& it = items[sp[m].idx];
         r.hi = std::max(r.hi, sp[m].hi);

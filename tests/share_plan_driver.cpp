@@ -45,6 +45,7 @@ int main() {
     std::vector<Item> lm, norm;
     const int64_t tiles = sfe::plan_items(items.data(), n, share != 0, &lm, &norm);
     std::map<int64_t, Key> raw;
+    std::map<int64_t, int> members;  // items per shared region
     int64_t quads = 0, own = 0;
     int32_t units = 0;
     for (const Item& e : lm) {
@@ -74,11 +75,16 @@ int main() {
         printf("case %d item %d: T or dst_off changed\n", k, i);
         ++bad;
       }
-      // the normalisation kernel's 32-bit byte offsets from the shared region
+      // the normalisation kernel's 32-bit buffer offsets from the shared
+      // region: every load below kNormBufRange bytes
       const int64_t span = std::max(it.out_off, it.tail_off) - it.grid_off + sfe::raw_frame(it.T + 64);
       if (it.out_off < it.grid_off || it.tail_off < it.grid_off ||
-          4 * (span + sfe::raw_frame((int64_t)it.gshift + 64)) >= ((int64_t)1 << 32)) {
-        printf("case %d item %d: regions beyond 32-bit offsets of the shared region\n", k, i);
+          4 * (span + sfe::raw_frame((int64_t)it.gshift + 64)) >= (int64_t)sfe::kNormBufRange) {
+        printf("case %d item %d: regions beyond the offsets of the shared region\n", k, i);
+        ++bad;
+      }
+      if (it.f_lo > 0 && ++members[it.grid_off] > sfe::kMaxShareMembers) {
+        printf("case %d item %d: more than kMaxShareMembers items share one region\n", k, i);
         ++bad;
       }
       if (it.f_lo > 0 && it.f_hi - it.f_lo + 1 > sfe::kMaxShareFrames) ++bad;
@@ -106,7 +112,8 @@ int main() {
       printf("case %d: sharing computes more quads (%lld > %lld)\n", k, (long long)quads, (long long)own);
       ++bad;
     }
-    printf("case %d quads %lld %lld tiles %lld\n", k, (long long)quads, (long long)own, (long long)tiles);
+    printf("case %d quads %lld %lld tiles %lld regions %zu\n", k, (long long)quads, (long long)own, (long long)tiles,
+           members.size());
     ++k;
   }
   printf("bad %ld\n", bad);

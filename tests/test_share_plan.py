@@ -51,6 +51,8 @@ def _cases():
     cases.append([(160 * i, 160 * 33 + 255 + i) for i in range(0, 200, 7)])
     cases.append([(0, 1), (0, 255), (0, 256), (0, 257), (160, 5536), (320, 5536)])
     cases.append([(0, 57_600_000)])
+    # 40,000 copies of one task: runs are cut at kMaxShareMembers (16384) members
+    cases.append([(1600, 16_000)] * 40_000)
     return cases
 
 
@@ -79,3 +81,5 @@ def test_shared_frames_plan(tmp_path):
     assert shared[5][0] < 0.88 * shared[5][1] and shared[6] == shared[4]
     # back-to-back clips: nothing shared
     assert shared[7][0] == shared[7][1]
+    # the copies: three shared regions
+    assert int(res[len(cases) - 1][8]) == 3 and shared[-1][0] < shared[-1][1]
