@@ -738,10 +738,13 @@ __device__ __forceinline__ void stage(float* tb, int q, int col, const float4& v
 }
 
 // W waves, slab of F features, N float4 registers per lane: items of up to
-// kSpan * N frames are held in registers and read once; longer items take
-// the streaming path (three passes, the later ones mostly cache hits).
-// `work` is the (item, slab) index.
-template <int W, int F, int N, typename O>
+// kSpan * N frames are held in registers and read once; the X rounds after
+// those (a multiple of 8) are read again for the variance and the stores
+// (mostly cache hits), and longer items take the streaming path (three
+// passes).  Every path sums the same rounds in the same groups of
+// kNormFlush, so the class does not change the result.  `work` is the
+// (item, slab) index.
+template <int W, int F, int N, int X, typename O>
 __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const Item* __restrict__ items,
                                           int n_items, int work, int pad_to, O* __restrict__ out) {
   static_assert(N % 4 == 0, "whole chunks");
@@ -802,7 +805,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   double s[4] = {0.0, 0.0, 0.0, 0.0}, sq[4] = {0.0, 0.0, 0.0, 0.0};
   bool eq[4] = {true, true, true, true};
   if constexpr (N > 0) {
-    if (T <= kSpan * N) {
+    if (T <= kSpan * (N + X)) {
       float4 v[N];
       // Raw buffer loads from the uniform base, all issued before any is
       // used (a load under a per-lane branch would wait for itself).  Rounds
@@ -830,6 +833,38 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
           }
         }
       }
+      // Round j >= N, loaded again in each pass.  The round index passes
+      // through an empty asm so that the offset and the lane test are
+      // computed afresh in each pass: shared between passes, they stay live
+      // over the whole kernel (one VGPR and one lane mask per round).
+      auto reload = [&](int j) -> float4 {
+        asm volatile("" : "+s"(j));
+        const int o = (int)(j < nr ? roff(j) : kNormBufRange);
+        const float4 e = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o, 0, 0));
+        return j < nr ? ln2_scale(e) : x0;
+      };
+      if constexpr (X > 0) {
+        static_assert(N % kNormFlush == 0 && X % kNormFlush == 0, "whole flush groups");
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+        for (int g = 0; g < X / 4; ++g) {
+          float4 e[4];
+#pragma unroll
+          for (int jr = 0; jr < 4; ++jr) e[jr] = reload(N + 4 * g + jr);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int jr = 0; jr < 4; ++jr) {
+              if (N + 4 * g + jr < nr) a[c] += comp(e[jr], c) - comp(x0, c);
+              eq[c] = eq[c] && (comp(e[jr], c) == comp(x0, c));
+            }
+            if ((4 * g + 4) % kNormFlush == 0) {
+              s[c] += (double)a[c];
+              a[c] = 0.0f;
+            }
+          }
+        }
+      }
       slab_sum<W, F>(s, red, lane, w);
       slab_all<W, F>(eq, redi, lane, w);
 #pragma unroll
@@ -846,14 +881,42 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
           }
         }
       }
+      if constexpr (X > 0) {
+        float m[4], a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) m[c] = (float)((double)comp(x0, c) + s[c] / (double)T);
+#pragma unroll 1
+        for (int g = 0; g < X / 4; ++g) {
+          float4 e[4];
+#pragma unroll
+          for (int jr = 0; jr < 4; ++jr) e[jr] = reload(N + 4 * g + jr);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int jr = 0; jr < 4; ++jr) {
+              const float d = comp(e[jr], c) - m[c];
+              if (N + 4 * g + jr < nr) a[c] += d * d;
+            }
+            if ((4 * g + 4) % kNormFlush == 0) {
+              sq[c] += (double)a[c];
+              a[c] = 0.0f;
+            }
+          }
+        }
+      }
       slab_sum<W, F>(sq, red, lane, w);
       publish_stats<F>(s, sq, eq, x0, T, lane, w, st);
       const int chunks = (T + kChunk - 1) / kChunk;
 #pragma unroll
-      for (int ch = 0; ch < N / 4; ++ch) {
+      for (int ch = 0; ch < (N + X) / 4; ++ch) {
         if (ch < chunks) {
+          if (ch < N / 4) {
 #pragma unroll
-          for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, v[4 * ch + jr]);
+            for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, v[4 * ch + jr]);
+          } else {
+#pragma unroll
+            for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, reload(4 * ch + jr));
+          }
           __syncthreads();
           store_chunk<W, F>(tb, st, kChunk * ch, T, rs, lane, w, ob);
           __syncthreads();
@@ -934,11 +997,11 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 constexpr int kNormMainWaves = 4;
 constexpr int kNormMainSlab = 16;
 
-template <int N, typename O>
+template <int N, int X, typename O>
 __global__ __launch_bounds__(64 * kNormMainWaves) void sfe_norm_kernel(const float* __restrict__ raw,
                                                                        const Item* __restrict__ items, int n_items,
                                                                        int pad_to, O* __restrict__ out) {
-  norm_body<kNormMainWaves, kNormMainSlab, N>(raw, items, n_items, blockIdx.x, pad_to, out);
+  norm_body<kNormMainWaves, kNormMainSlab, N, X>(raw, items, n_items, blockIdx.x, pad_to, out);
 }
 
 // Calls of few items (a clip, a small batch) leave most CUs idle with 4-wave
@@ -953,7 +1016,7 @@ __global__ __launch_bounds__(64 * kNormWideWaves) void sfe_norm_wide_kernel(cons
                                                                             const Item* __restrict__ items,
                                                                             int n_items, int pad_to,
                                                                             O* __restrict__ out) {
-  norm_body<kNormWideWaves, kNormMainSlab, N>(raw, items, n_items, blockIdx.x, pad_to, out);
+  norm_body<kNormWideWaves, kNormMainSlab, N, 0>(raw, items, n_items, blockIdx.x, pad_to, out);
 }
 
 }  // namespace
@@ -1012,11 +1075,15 @@ hipError_t launch_norm_t(const float* raw, const Item* items, int n_items, int m
   }
   const dim3 grid(blocks), block(S::kThreads);
   // Registers per lane sized to the longest item (N float4s hold kSpan N
-  // frames); longer items take the streaming path.
-  if (max_T <= S::kSpan * 8) sfe_norm_kernel<8, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
-  else if (max_T <= S::kSpan * 16) sfe_norm_kernel<16, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
-  else if (max_T <= S::kSpan * 24) sfe_norm_kernel<24, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
-  else sfe_norm_kernel<32, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  // frames); items of up to 2048 frames keep 1536 in registers (32 rounds
+  // in registers need 184 VGPRs, 2 workgroups per CU instead of 3), longer
+  // ones take the streaming path.
+  if (max_T <= S::kSpan * 8) sfe_norm_kernel<8, 0, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  else if (max_T <= S::kSpan * 16)
+    sfe_norm_kernel<16, 0, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  else if (max_T <= S::kSpan * 24)
+    sfe_norm_kernel<24, 0, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
+  else sfe_norm_kernel<24, 8, O><<<grid, block, 0, stream>>>(raw, items, n_items, pad_to, out);
   return hipGetLastError();
 }
 

@@ -625,3 +625,28 @@ def test_config3_shared_frames_equal_own_frames(extractor):
     finally:
         extractor.set_frame_sharing(True)
     assert torch.equal(a, b)
+
+
+def test_norm_class_does_not_change_results(extractor):
+    """The normalisation kernel's register class follows the batch's longest
+    item (16, 24 or 24 + 8 rounds of 64 frames in registers, or the
+    streaming path past 2048 frames); every class sums the same rounds in the
+    same groups, so 17 clips give bitwise the same features whichever longer
+    clip joins their batch (17 clips: past the 8-wave few-item variant)."""
+    import torch
+    rng = np.random.default_rng(77)
+    lens = [int(v) for v in rng.integers(16_000, 160_000, 17)]  # at most 1000 frames
+    base = None
+    for extra in (None, 192_000, 288_000, 400_000):  # 1201, 1801, 2501 frames
+        _flush(f"case: norm class, extra clip {extra}")
+        ls = lens + ([extra] if extra else [])
+        off = np.concatenate([[0], np.cumsum(ls)]).astype(np.int64)
+        flat = synth.speech_like(int(off[-1]), 12)
+        flat[:off[17]] = synth.speech_like(int(off[17]), 13)  # the 17 clips' samples equal in every batch
+        out, fo = extractor.extract_batch(torch.from_numpy(flat).cuda(), off)
+        torch.cuda.synchronize()
+        got = out[:128 * int(fo[17])].cpu()
+        if base is None:
+            base = got
+        else:
+            assert torch.equal(got, base), extra
