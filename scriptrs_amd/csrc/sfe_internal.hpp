@@ -95,13 +95,11 @@ inline Item own_item(int64_t start, int64_t len, int64_t out_off, int64_t dst_of
 // hop are computed once: items' own regions keep only their first quad and
 // their last quads, and a shared log-mel entry per run of such items covers
 // the union of their interior frames.  Given items with their own regions
-// (own_item; out_off ignored), fills the log-mel and normalisation tables
-// and returns the raw tiles they use.  With share = false, or where sharing
-// saves no quads, every item keeps its own region.
-int64_t plan_items(const Item* items, int n, bool share, std::vector<Item>* lm, std::vector<Item>* norm);
-// The same into one table without allocating: table[0, *n_lm) gets the
-// log-mel entries, table[*n_lm, *n_lm + n) the normalisation entries in item
-// order.  table holds (kPlanEntriesPerItem + 1) n entries; nothing is
+// (own_item; out_off ignored), plan_table fills one table, table[0, *n_lm)
+// with the log-mel entries and table[*n_lm, *n_lm + n) with the
+// normalisation entries in item order, and returns the raw tiles they use.
+// With share = false, or where sharing saves no quads, every item keeps its
+// own region.  table holds (kPlanEntriesPerItem + 1) n entries; nothing is
 // allocated when ws was reserved for at least n items.
 constexpr int kPlanEntriesPerItem = 3;  // log-mel entries per item at most
 struct PlanWorkspace {

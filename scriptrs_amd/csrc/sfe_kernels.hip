@@ -770,9 +770,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   static_assert(F == 16 && S::kGroup == 16, "one wave's load covers one tile of one slab");
   // Loads address a uniform base (the start of the item's shared frames,
   // this slab) plus a 32-bit per-lane byte offset: an item's own first and
-  // last tiles come after its shared region, which holds at most
-  // kMaxShareFrames frames, and an item with its own region has all three
-  // at out_off.  The region is chosen by adding differences under
+  // last tiles come after its shared region (at most kMaxShareFrames
+  // frames, then at most 3 tiles for each of at most kMaxShareMembers
+  // members), and an item with its own region has all three at out_off.  The region is chosen by adding differences under
   // conditions (a choice among several values compiles to a table in
   // private memory).  The own first tile holds frames below f_lo <= 16, so
   // only round 0 can reach it.

@@ -218,15 +218,4 @@ void order_norm(Item* norm, int n) {
   });
 }
 
-int64_t plan_items(const Item* items, int n, bool share, std::vector<Item>* lm, std::vector<Item>* norm) {
-  PlanWorkspace ws;
-  ws.reserve((size_t)n);
-  std::vector<Item> table((size_t)(kPlanEntriesPerItem + 1) * n);
-  size_t n_lm = 0;
-  const int64_t tiles = plan_table(items, n, share, &ws, table.data(), &n_lm);
-  lm->assign(table.begin(), table.begin() + (ptrdiff_t)n_lm);
-  norm->assign(table.begin() + (ptrdiff_t)n_lm, table.begin() + (ptrdiff_t)(n_lm + (size_t)n));
-  return tiles;
-}
-
 }  // namespace sfe

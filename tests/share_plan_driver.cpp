@@ -1,12 +1,15 @@
-// Checks sfe::plan_items (scriptrs_amd/csrc/sfe_share.cpp) on the host: every
-// frame that the normalisation kernel reads for an item must be a raw slot
-// that a log-mel entry writes, with exactly the padded samples that the item
-// itself would have used for that frame.
+// Checks sfe::plan_table and sfe::order_norm (scriptrs_amd/csrc/sfe_share.cpp)
+// on the host: every frame that the normalisation kernel reads for an item
+// must be a raw slot that a log-mel entry writes, with exactly the padded
+// samples that the item itself would have used for that frame; the
+// reordered normalisation entries are a permutation of the planned ones.
 //
 // stdin: cases, each "n share" then n lines "start len".  For each case
 // prints "case <k> quads <with> <own> tiles <t>" and at the end "bad <count>".
 #include <stdio.h>
+#include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <tuple>
 #include <vector>
@@ -42,8 +45,49 @@ int main() {
       items[i] = sfe::own_item(s, l, 0, sfe::kMel * fo, 0);
       fo += items[i].T;
     }
-    std::vector<Item> lm, norm;
-    const int64_t tiles = sfe::plan_items(items.data(), n, share != 0, &lm, &norm);
+    sfe::PlanWorkspace ws;
+    ws.reserve((size_t)n);
+    std::vector<Item> table((size_t)(sfe::kPlanEntriesPerItem + 1) * n);
+    size_t n_lm = 0;
+    const size_t cap[4] = {ws.sp.capacity(), ws.run_of.capacity(), ws.runs.capacity(), ws.pieces.capacity()};
+    const int64_t tiles = sfe::plan_table(items.data(), n, share != 0, &ws, table.data(), &n_lm);
+    const size_t cap2[4] = {ws.sp.capacity(), ws.run_of.capacity(), ws.runs.capacity(), ws.pieces.capacity()};
+    for (int c = 0; c < 4; ++c)
+      if (cap2[c] != cap[c]) {
+        printf("case %d: planner list %d grew past reserve(n)\n", k, c);
+        ++bad;
+      }
+    if (n_lm > (size_t)sfe::kPlanEntriesPerItem * n) {
+      printf("case %d: %zu log-mel entries for %d items\n", k, n_lm, n);
+      ++bad;
+    }
+    const std::vector<Item> lm(table.begin(), table.begin() + (ptrdiff_t)n_lm);
+    const std::vector<Item> norm(table.begin() + (ptrdiff_t)n_lm, table.begin() + (ptrdiff_t)(n_lm + n));
+    // order_norm: longest first in classes of 256 frames, output order
+    // within one, and the same entries
+    std::vector<Item> ordered(norm);
+    sfe::order_norm(ordered.data(), n);
+    for (int i = 0; i < n; ++i) {
+      const Item& a = ordered[i];
+      if (i > 0) {
+        const Item& p = ordered[i - 1];
+        if ((p.T >> 8) < (a.T >> 8) || ((p.T >> 8) == (a.T >> 8) && p.dst_off >= a.dst_off)) {
+          printf("case %d: normalisation order broken at %d\n", k, i);
+          ++bad;
+        }
+      }
+    }
+    {
+      // the same entries, byte for byte (dst_off differs between items)
+      auto by_dst = [](const Item& a, const Item& b) { return a.dst_off < b.dst_off; };
+      std::vector<Item> x(norm), y(ordered);
+      std::sort(x.begin(), x.end(), by_dst);
+      std::sort(y.begin(), y.end(), by_dst);
+      if (memcmp(x.data(), y.data(), x.size() * sizeof(Item)) != 0) {
+        printf("case %d: reordered normalisation entries differ\n", k);
+        ++bad;
+      }
+    }
     std::map<int64_t, Key> raw;
     std::map<int64_t, int> members;  // items per shared region
     int64_t quads = 0, own = 0;
