@@ -650,3 +650,51 @@ def test_norm_class_does_not_change_results(extractor):
             base = got
         else:
             assert torch.equal(got, base), extra
+
+
+def test_random_tables_shared_equal_own_bitwise(extractor):
+    """150 random task tables over one 500 s recording (hop-aligned,
+    arbitrary, clustered and duplicated starts; lengths 1 sample to 15 s):
+    sharing on and off, and the allocation-free entry point, give bitwise the
+    same features (compared as bits: 1-frame tasks are NaN, as in the
+    reference, src/frontend.rs:225-241)."""
+    import torch
+    from scriptrs_amd import TaskTable
+    _flush("case: 150 random tables, shared vs own")
+    rng = np.random.default_rng(2024)
+    rec = synth.speech_like(8_000_000, 5)
+    dev = torch.from_numpy(rec).cuda()
+
+    def bits_equal(x, y):
+        return torch.equal(x.view(torch.int32), y.view(torch.int32))
+
+    try:
+        for case in range(150):
+            kind = case % 4
+            n = int(rng.integers(1, 300))
+            tasks = []
+            for _ in range(n):
+                L = int(rng.integers(1, 240_001)) if rng.random() < 0.9 else int(rng.integers(1, 2000))
+                if kind == 0:
+                    s = 160 * int(rng.integers(0, (rec.size - L) // 160 + 1))
+                elif kind == 1:
+                    s = int(rng.integers(0, rec.size - L + 1))
+                elif kind == 2:
+                    s = min(rec.size - L, 160 * 16000 * int(rng.integers(0, 20)) + 160 * int(rng.integers(0, 4000)))
+                else:
+                    s = min(rec.size - L, 160 * 800 * int(rng.integers(0, 50)))
+                tasks.append((s, s + L, s, 0))
+            if kind == 3:
+                tasks += tasks[: n // 2]
+            tt = TaskTable(np.array(tasks, np.int64))
+            extractor.set_frame_sharing(True)
+            a, fa = extractor.extract_chunks(dev, tt)
+            c, fc = extractor.extract_chunks_noalloc(dev, tt) if int(tt.frame_offsets[-1]) < 100_000 else (a, fa)
+            extractor.set_frame_sharing(False)
+            b, fb = extractor.extract_chunks(dev, tt)
+            torch.cuda.synchronize()
+            assert np.array_equal(fa, fb) and np.array_equal(fa, fc), case
+            assert bits_equal(a, b), f"case {case} kind {kind}: shared != own"
+            assert bits_equal(a, c), f"case {case} kind {kind}: noalloc != extract_chunks"
+    finally:
+        extractor.set_frame_sharing(True)
