@@ -189,20 +189,24 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
                               void* stream);
 
 /* Allocation-free variant of sfe_extract_chunks.  No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  It runs the same kernels as sfe_extract_chunks, with the same
- * results (frames that tasks share computed once, as there), but keeps its
- * item table and raw log-mel in a static device array
- * of the library (one per GPU, held until the process ends) instead of the
- * context's growable buffers, and calls no hipMalloc, hipFree or other
- * allocating routine.  Limits: at most 4096 tasks, and at most 64 MiB of raw
- * log-mel, which is 8192 tiles of 16 frames per task rounded up (131,072
- * frames, about 22 minutes of audio in 15 s chunks); larger calls return
- * SFE_INVALID_ARG.  Every call on one GPU shares that array, from every
- * context: calls that overlap on one GPU (several host threads or contexts
- * on one device without ordering between them) race.  Calls on one context
- * are ordered.  Arguments, outputs and errors as sfe_extract_chunks. */
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  It runs the same kernels
+ * as sfe_extract_chunks, with the same results (frames that tasks share
+ * computed once, as there), but keeps its item table and raw log-mel in a
+ * static device array of the library (one per GPU, held until the process
+ * ends) instead of the context's growable buffers, and calls no hipMalloc,
+ * hipFree or other allocating routine (sfe_create reserves the host
+ * buffers its planner uses, about 1.3 MB of pinned memory per context).
+ * Limits: at most 4096 tasks, and at most 64 MiB of raw log-mel, which is
+ * 8192 tiles of 16 frames per task rounded up (131,072 frames, about 22
+ * minutes of audio in 15 s chunks); larger calls return SFE_INVALID_ARG.
+ * Every call on one GPU shares that array, from every context: the library
+ * serialises such calls on the host and orders them on the device (an event
+ * per GPU), so calls from several threads, contexts or streams do not race;
+ * they do not overlap on the device either.  It cannot be captured into a
+ * HIP graph (its item-table upload reads a pinned buffer that the next call
+ * rewrites): on a capturing stream it returns SFE_INVALID_ARG.  Arguments,
+ * outputs and errors otherwise as sfe_extract_chunks. */
 int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len, const sfe_chunk* tasks, int32_t n,
                                int32_t out_dtype, void* out, int64_t* frame_offsets, void* stream);
 
@@ -261,6 +265,12 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
  * the setting too.  Returns
  * SFE_INVALID_ARG for a null ctx. */
 int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
+
+/* Test hook, no counterpart in the reference: the number of device and
+ * pinned host allocations (hipMalloc, hipHostMalloc) the library has made in
+ * this process, over all contexts.  It lets a test check that a call
+ * allocated nothing. */
+int64_t sfe_debug_allocation_count(void);
 
 /* Turn per-kernel timing on or off for ctx.  When on, every launch of the
  * log-mel and normalisation kernels is bracketed by HIP events on the stream

@@ -62,16 +62,44 @@ def mfma_operand_overlaps(asm: str) -> list[str]:
     return bad
 
 
-def check_mfma(src: str, extra: list[str], verbose: bool = False) -> None:
+def lane_masked_loops(asm: str, kernel: str) -> int:
+    """Loops of ``kernel`` in ``asm`` whose trip is controlled per lane (the
+    back edge masks lanes out of exec: ``s_andn2_b64 exec, exec, ...``)."""
+    m = re.search(r"^(_Z\S*" + kernel + r"\S*):", asm, re.M)
+    if not m:
+        raise RuntimeError(f"kernel {kernel} not found in the generated assembly")
+    body = asm[m.start():asm.index(".Lfunc_end", m.start())]
+    return body.count("s_andn2_b64 exec, exec")
+
+
+# The log-mel kernels' work loop takes its units through a lane-0 counter
+# broadcast with readfirstlane, which is only sound while all 64 lanes go
+# round the loop together.  The compiler may instead structurise a loop with
+# lane-conditional code into a per-lane (exec-masked) loop in which lanes
+# leave at different iterations; a handoff probe built that way looped
+# forever.  The only per-lane loop these kernels may have is the copy of the
+# mel A operands into LDS (a strided per-thread loop, in the 4-wave form).
+LANE_LOOP_LIMITS = {"sfe_logmel_kernelI[fsi]Li12E": 0, "sfe_logmel_kernelI[fsi]Li4E": 1}
+
+
+def check_asm(src: str, extra: list[str], verbose: bool = False) -> None:
     with tempfile.TemporaryDirectory() as tmp:
         out = os.path.join(tmp, "k.s")
         cmd = [HIPCC, *COMMON, *extra, "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", out]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True, stderr=subprocess.DEVNULL)
-        bad = mfma_operand_overlaps(open(out).read())
+        asm = open(out).read()
+    bad = mfma_operand_overlaps(asm)
     if bad:
         raise RuntimeError(f"{src}: MFMA destination overlaps its own A/B operand:\n  " + "\n  ".join(bad))
+    for pat, limit in LANE_LOOP_LIMITS.items():
+        for t in "fsi":
+            k = pat.replace("[fsi]", t)
+            n = lane_masked_loops(asm, k)
+            if n > limit:
+                raise RuntimeError(f"{src}: {k} has {n} per-lane loops (at most {limit}): its work loop "
+                                   "must stay a wave-uniform loop")
 
 
 def build(verbose: bool = False) -> str:
@@ -85,7 +113,7 @@ def build(verbose: bool = False) -> str:
         subprocess.run(cmd, check=True)
         objs.append(obj)
         if src in MFMA_CHECKED:
-            check_mfma(src, extra, verbose)
+            check_asm(src, extra, verbose)
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <exception>
 #include <mutex>
 #include <new>
@@ -73,6 +74,10 @@ void parallel_memcpy(void* dst, const void* src, size_t bytes) {
 
 thread_local std::string g_last_error;
 
+// Device and pinned host allocations made by the library (every hipMalloc
+// and hipHostMalloc below counts one), read by sfe_debug_allocation_count.
+std::atomic<int64_t> g_allocations{0};
+
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
   return code;
@@ -102,6 +107,7 @@ struct DevBuf {
     ptr = nullptr;
     cap = 0;
     e = hipMalloc(&ptr, want);
+    g_allocations.fetch_add(1);
     if (e == hipSuccess) cap = want;
     return e;
   }
@@ -136,6 +142,7 @@ struct PinBuf {
     cap = 0;
     size_t want = std::max(bytes, (size_t)4096);
     e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
+    g_allocations.fetch_add(1);
     if (e == hipSuccess) cap = want;
     return e;
   }
@@ -178,6 +185,8 @@ struct sfe_ctx {
   // and the raw scratch): see order_after_last.
   hipEvent_t ev_last = nullptr;
   bool has_last = false;
+  bool last_marked = false;   // ev_last marks the end of the previous call
+  bool multi_stream = false;  // calls have come on more than one stream
   hipStream_t last_stream = nullptr;  // the stream the previous call's device work ran on
   PinBuf h_meta;
   DevBuf scratch;   // raw log-mel in 16-frame tiles, f32 (the normalisation kernel's input)
@@ -217,20 +226,32 @@ struct sfe_ctx {
 namespace {
 
 // Orders this call's work on `stream` after the context's previous call (the
-// calls share the item table and the raw scratch).  On the stream that call
-// used, stream order already does; an event there would cost the device a
-// barrier between the calls' kernels.  On another stream, an event recorded
-// now on the previous call's stream (after everything enqueued there so far,
-// that call included) is waited on.
+// calls share the item table and the raw scratch).  Nothing is ever enqueued
+// on an earlier call's stream, which its owner may have destroyed since.
+// * Same stream: stream order is enough.
+// * Another stream, previous call marked by ev_last: wait for that event.
+// * Another stream, previous call unmarked: a context whose calls have all
+//   been on one stream records no event (a marker after every call costs
+//   launch-bound calls about 3 us: one 10 s clip 0.0156 -> 0.0189 ms), so the
+//   first switch waits on the host for the device to drain (work on a
+//   destroyed stream included), and from then on every call records ev_last.
 hipError_t order_after_last(sfe_ctx* ctx, hipStream_t stream) {
   if (!ctx->has_last || stream == ctx->last_stream) return hipSuccess;
-  hipError_t e = hipEventRecord(ctx->ev_last, ctx->last_stream);
-  if (e != hipSuccess) return e;
-  return hipStreamWaitEvent(stream, ctx->ev_last, 0);
+  if (ctx->last_marked) return hipStreamWaitEvent(stream, ctx->ev_last, 0);
+  ctx->multi_stream = true;
+  return hipDeviceSynchronize();
 }
 
-// The call just enqueued ran on `stream` (no device work is added).
+// The call just enqueued ran on `stream`; a context that has used more than
+// one stream marks its end there with ev_last.
 hipError_t mark_last(sfe_ctx* ctx, hipStream_t stream) {
+  ctx->has_last = false;
+  ctx->last_marked = false;
+  if (ctx->multi_stream) {
+    hipError_t e = hipEventRecord(ctx->ev_last, stream);
+    if (e != hipSuccess) return e;
+    ctx->last_marked = true;
+  }
   ctx->has_last = true;
   ctx->last_stream = stream;
   return hipSuccess;
@@ -518,6 +539,7 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
       sfe_destroy(ctx);
       return rc;
     };
+    g_allocations.fetch_add(1);
     if ((e = hipMalloc(&ctx->d_tables, sizeof(sfe::DevTables))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc"));
     if ((e = hipMemcpy(ctx->d_tables, &host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
       return cleanup(hip_fail(e, "hipMemcpy"));
@@ -737,6 +759,19 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
       return fail(SFE_INVALID_ARG, "sfe_extract_chunks_noalloc: the tasks need " + std::to_string(raw_bytes) +
                                        " bytes of scratch, more than its " + std::to_string(sfe::kNoAllocRawBytes));
     if ((rc = check_ctx(ctx))) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // Not under stream capture: the pinned item table a captured copy would
+    // read is rewritten by every later call on the context, so a replay
+    // would upload another call's table.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SFE_HIP(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(SFE_INVALID_ARG, "sfe_extract_chunks_noalloc cannot be captured into a graph");
+    // Calls on one device share its static scratch: the device lock orders
+    // them on the host, and its event orders them on the device, whatever
+    // context or stream they come from.
+    std::unique_lock<std::mutex> dev_lock;
+    SFE_HIP(sfe::noalloc_lock(ctx->device, &dev_lock));
     std::lock_guard<std::mutex> lock(ctx->mu);
     const size_t entries = (size_t)(sfe::kPlanEntriesPerItem + 1) * n;
     if (!ctx->noalloc || ctx->h_meta.cap < entries * sizeof(Item) || ctx->na_in.capacity() < (size_t)n)
@@ -760,8 +795,8 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     tiles = sfe::plan_table(ctx->na_in.data(), n, share, &ctx->na_ws, table, &n_lm);
     if (share && tiles > own_tiles) tiles = sfe::plan_table(ctx->na_in.data(), n, false, &ctx->na_ws, table, &n_lm);
     sfe::order_norm(table + n_lm, n);
-    hipStream_t s = static_cast<hipStream_t>(stream);
     SFE_HIP(order_after_last(ctx, s));
+    SFE_HIP(sfe::noalloc_order(ctx->device, s));
     Item* d_table = reinterpret_cast<Item*>(ctx->noalloc);
     float* raw = reinterpret_cast<float*>(ctx->noalloc + sfe::kNoAllocItemBytes);
     SFE_HIP(hipMemcpyAsync(d_table, table, (n_lm + n) * sizeof(Item), hipMemcpyHostToDevice, s));
@@ -771,6 +806,7 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
                      out_dtype, 0, s, kBoth, false);
     if (rc) return rc;
     SFE_HIP(mark_last(ctx, s));
+    SFE_HIP(sfe::noalloc_mark(ctx->device, s));
     return SFE_OK;
   });
 }
@@ -985,6 +1021,8 @@ int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable) {
   ctx->share = enable != 0;
   return SFE_OK;
 }
+
+int64_t sfe_debug_allocation_count(void) { return g_allocations.load(); }
 
 int sfe_set_timing(sfe_ctx* ctx, int32_t enable) {
   if (!ctx) return fail(SFE_INVALID_ARG, "null context");

@@ -1,6 +1,8 @@
 // Internal declarations shared by the kernels and the C-ABI layer.
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <stdint.h>
 
 #include <vector>
@@ -194,6 +196,13 @@ constexpr size_t kNoAllocItemBytes =
 constexpr size_t kNoAllocRawBytes = (size_t)64 << 20;
 // Device address of this device's static scratch (looked up once per device).
 hipError_t noalloc_scratch(int device, void** out);
+// Host lock of a device's static scratch (held for a whole call), and the
+// device-side order of calls on it: noalloc_order makes `stream` wait for
+// the previous call's end when that call ran on another stream, noalloc_mark
+// records this call's end on `stream`.  Both need the lock held.
+hipError_t noalloc_lock(int device, std::unique_lock<std::mutex>* lock);
+hipError_t noalloc_order(int device, hipStream_t stream);
+hipError_t noalloc_mark(int device, hipStream_t stream);
 
 // Silero VAD model inputs (sfe_vad.hip): [64 context | 512 window] f32 per
 // 512-sample window (src/long_form/vad.rs:62-99, src/constants.rs).

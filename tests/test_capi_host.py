@@ -230,6 +230,17 @@ def test_build_rejects_mfma_destination_overlapping_its_operands():
     assert len(bad) == 2 and "v49" in bad[0] and "v51" in bad[1]
 
 
+def test_build_counts_lane_masked_loops_per_kernel():
+    from scriptrs_amd.build import lane_masked_loops
+    asm = ("_ZN3sfe4kernAEv:\n\ts_andn2_b64 exec, exec, s[4:5]\n\ts_cbranch_execnz .LBB0_1\n"
+           "\ts_andn2_b64 exec, exec, s[8:9]\n.Lfunc_end0:\n"
+           "_ZN3sfe4kernBEv:\n\ts_cbranch_scc1 .LBB1_1\n.Lfunc_end1:\n")
+    assert lane_masked_loops(asm, "kernA") == 2
+    assert lane_masked_loops(asm, "kernB") == 0
+    with pytest.raises(RuntimeError):
+        lane_masked_loops(asm, "kernC")
+
+
 def _closed_form_plan(n, chunk=238_080, stride=206_080, ctx=1280, hop=160):
     """Count, sum of task lengths and sum of frame counts of the fast plan,
     in closed form: task i covers [max(i*stride - ctx, 0), min(i*stride +

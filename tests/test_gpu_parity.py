@@ -356,6 +356,35 @@ def test_calls_on_two_streams_and_repeated_plans(extractor):
         assert torch.equal(oa2, want_a)
 
 
+def test_call_after_the_previous_calls_stream_was_destroyed(extractor):
+    """A caller may destroy a stream right after a call on it (per-request
+    streams).  The next call, on another stream, is still ordered after the
+    first (they share the context's item table and raw scratch) and nothing
+    is enqueued on the destroyed stream."""
+    import ctypes
+    import torch
+    from scriptrs_amd import TaskTable, build_fast_execution_plan
+    _flush("case: previous call's stream destroyed")
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch has loaded
+    ra = synth.speech_like(1_200_000, 44)
+    rb = synth.speech_like(700_000, 45)
+    ta = TaskTable(build_fast_execution_plan(ra.size))
+    tb = TaskTable(build_fast_execution_plan(rb.size))
+    da, db = torch.from_numpy(ra).cuda(), torch.from_numpy(rb).cuda()
+    want_a, _ = extractor.extract_chunks(da, ta)
+    want_b, _ = extractor.extract_chunks(db, tb)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        s = ctypes.c_void_p()
+        assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+        oa, _ = extractor.extract_chunks(da, ta, stream=s.value)
+        assert hip.hipStreamDestroy(s) == 0
+        ob, _ = extractor.extract_chunks(db, tb)  # torch's current stream
+        torch.cuda.synchronize()
+        assert torch.equal(oa, want_a), rep
+        assert torch.equal(ob, want_b), rep
+
+
 @pytest.mark.parametrize("n", [327_680, 327_840, 480_000])
 def test_items_longer_than_register_budget(extractor, n):
     """T > 2048 frames takes the normalisation kernel's streaming path

@@ -97,3 +97,89 @@ def test_noalloc_shared_plan_at_its_raw_limit(extractor):
     finally:
         extractor.set_frame_sharing(True)
     assert torch.equal(outs[0], outs[1])
+
+
+def test_noalloc_allocates_nothing_on_a_fresh_context():
+    """The contract itself: after sfe_create, calls of the allocation-free
+    entry point make no device or pinned host allocation (the library counts
+    every hipMalloc and hipHostMalloc it makes), on a fresh context, over
+    calls of different sizes."""
+    import torch
+    from scriptrs_amd import ParakeetFeatureExtractor
+    _flush("case: noalloc allocation count on a fresh context")
+    L = _lib.lib()
+    stream = torch.cuda.current_stream()
+    rec = synth.speech_like(1_440_000, 41)
+    big = TaskTable(build_fast_execution_plan(rec.size))
+    small = TaskTable([ChunkTask(0, 300_000, 0, 0), ChunkTask(1000, 2000, 1000, 0)])
+    dev = torch.from_numpy(rec).cuda()
+    out = torch.empty(int(big.frame_offsets[-1]) * 128, dtype=torch.float32, device="cuda")
+    ext = ParakeetFeatureExtractor()
+    try:
+        ctx = ext._handle()
+        before = L.sfe_debug_allocation_count()
+        for tt in (big, small, big):
+            rc, _ = _noalloc(ctx, dev, tt, out, _lib.SFE_F32, stream)
+            assert rc == _lib.SFE_OK, _lib.last_error()
+        torch.cuda.synchronize()
+        assert L.sfe_debug_allocation_count() == before
+        # the counter does count: a resident call on the same fresh context
+        # grows its item table and raw scratch
+        ext.extract_chunks(dev, big, stream=stream, out=out)
+        torch.cuda.synchronize()
+        assert L.sfe_debug_allocation_count() > before
+    finally:
+        ext.close()
+
+
+def test_noalloc_rejects_graph_capture(extractor):
+    """Its pinned item table is rewritten by every call, so a captured upload
+    would replay another call's table: under capture it returns
+    SFE_INVALID_ARG and enqueues nothing."""
+    import torch
+    _flush("case: noalloc under stream capture")
+    ctx = extractor._handle()
+    rec = synth.speech_like(240_000, 42)
+    tt = TaskTable([ChunkTask(0, rec.size, 0, 0)])
+    dev = torch.from_numpy(rec).cuda()
+    out = torch.empty(int(tt.frame_offsets[-1]) * 128, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        g.capture_begin(capture_error_mode="relaxed")
+        try:
+            rc, _ = _noalloc(ctx, dev, tt, out, _lib.SFE_F32, s)
+        finally:
+            g.capture_end()
+    assert rc == _lib.SFE_INVALID_ARG and "captured" in _lib.last_error()
+    torch.cuda.synchronize()
+
+
+def test_noalloc_calls_from_two_contexts_on_two_streams_do_not_race(extractor):
+    """Two contexts share the device's static scratch; calls issued back to
+    back on two streams, with no host synchronisation between them, must
+    each give sfe_extract_chunks' output bit for bit."""
+    import torch
+    from scriptrs_amd import ParakeetFeatureExtractor
+    _flush("case: noalloc two contexts, two streams")
+    recs = [synth.speech_like(1_440_000, 51), synth.speech_like(960_000, 52)]
+    tts = [TaskTable(build_fast_execution_plan(r.size)) for r in recs]
+    devs = [torch.from_numpy(r).cuda() for r in recs]
+    wants = [extractor.extract_chunks(d, t, dtype="f32")[0] for d, t in zip(devs, tts)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    exts = [ParakeetFeatureExtractor(), ParakeetFeatureExtractor()]
+    try:
+        outs = [[torch.full_like(w, float("nan")) for _ in range(3)] for w in wants]
+        for rep in range(3):
+            for k in (0, 1):
+                rc, _ = _noalloc(exts[k]._handle(), devs[k], tts[k], outs[k][rep], _lib.SFE_F32, streams[k])
+                assert rc == _lib.SFE_OK, _lib.last_error()
+        torch.cuda.synchronize()
+        for k in (0, 1):
+            for rep in range(3):
+                assert torch.equal(outs[k][rep], wants[k]), (k, rep)
+    finally:
+        for e in exts:
+            e.close()
