@@ -148,7 +148,9 @@ static_assert(kMaxShareFrames * kRawTile / kTile * 4 + (int64_t)kMaxShareMembers
 struct DevTables {
   float window[kNfft];       // hann_window(400), zero past 400
   float2 tw256[256];         // [l * 16 + k1] = e^{-2 pi i l k1 / 256}, l, k1 < 16
-  float2 tw512[256];         // e^{-2 pi i k / 512}, k < 256
+  // Split twiddles e^{-2 pi i k / 512}, k < 128, as (s, r): k < 64: (cos,
+  // tan); k >= 64: (sin, cos / sin) (sfe_fft.hpp split_g).
+  float2 split[128];
   // A operands of the mel MFMAs: [v][lane] holds steps 4v..4v+3 (v < 2:
   // chain 0, else chain 1, steps 4(v-2)..) of lane L = 4j + m: filter
   // 64c + 4j + m at bin k0[c][j] + step, times 0.25 (the FFT stage yields

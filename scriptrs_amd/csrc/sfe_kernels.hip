@@ -24,6 +24,7 @@
 // value.
 #include <hip/hip_runtime.h>
 
+#include "sfe_fft.hpp"
 #include "sfe_internal.hpp"
 #include "sfe_pcm.hpp"
 
@@ -39,79 +40,6 @@ constexpr int kXStride = 17;                         // transpose row stride (co
 constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
 constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
 constexpr float kLn2 = 0.69314718055994531f;
-
-struct __align__(8) cf {
-  float x, y;
-};
-
-__device__ __forceinline__ cf cadd(cf a, cf b) { return {a.x + b.x, a.y + b.y}; }
-__device__ __forceinline__ cf csub(cf a, cf b) { return {a.x - b.x, a.y - b.y}; }
-__device__ __forceinline__ cf cmul(cf a, cf w) { return {a.x * w.x - a.y * w.y, a.x * w.y + a.y * w.x}; }
-
-// Multiply by e^{-2 pi i j/16} for a compile-time j.
-template <int J>
-__device__ __forceinline__ cf tw16(cf a) {
-  constexpr float C1 = 0.92387953251128674f;  // cos(pi/8)
-  constexpr float S1 = 0.38268343236508978f;  // sin(pi/8)
-  constexpr float R = 0.70710678118654752f;   // sqrt(1/2)
-  if constexpr (J == 0) return a;
-  else if constexpr (J == 1) return {a.x * C1 + a.y * S1, a.y * C1 - a.x * S1};
-  else if constexpr (J == 2) return {R * (a.x + a.y), R * (a.y - a.x)};
-  else if constexpr (J == 3) return {a.x * S1 + a.y * C1, a.y * S1 - a.x * C1};
-  else if constexpr (J == 4) return {a.y, -a.x};
-  else if constexpr (J == 6) return {R * (a.y - a.x), -R * (a.x + a.y)};
-  else {
-    static_assert(J == 9, "unused twiddle");
-    return {-(a.x * C1 + a.y * S1), -(a.y * C1 - a.x * S1)};
-  }
-}
-
-// 4-point forward DFT in place on (a0, a1, a2, a3); when Z3 the caller
-// guarantees a3 == 0 and it is never read.
-template <bool Z3>
-__device__ __forceinline__ void dft4(cf& a0, cf& a1, cf& a2, cf& a3) {
-  cf t0 = cadd(a0, a2), t1 = csub(a0, a2);
-  cf t2 = Z3 ? a1 : cadd(a1, a3);
-  cf t3 = Z3 ? a1 : csub(a1, a3);
-  a0 = cadd(t0, t2);
-  a2 = csub(t0, t2);
-  a1 = {t1.x + t3.y, t1.y - t3.x};  // t1 - i t3
-  a3 = {t1.x - t3.y, t1.y + t3.x};  // t1 + i t3
-}
-
-// 16-point forward DFT in registers: in a[m] -> out a[k] (natural order).
-// m = p + 4q, k = c + 4d.  PRUNE: a[13], a[14], a[15] are zero.
-template <bool PRUNE>
-__device__ __forceinline__ void dft16(cf (&a)[16]) {
-  // inner 4-point DFTs over q for each p: U[p][c] stored at a[p + 4c]
-  dft4<false>(a[0], a[4], a[8], a[12]);
-  dft4<PRUNE>(a[1], a[5], a[9], a[13]);
-  dft4<PRUNE>(a[2], a[6], a[10], a[14]);
-  dft4<PRUNE>(a[3], a[7], a[11], a[15]);
-  // twiddles e^{-2 pi i p c / 16}
-  a[5] = tw16<1>(a[5]);
-  a[9] = tw16<2>(a[9]);
-  a[13] = tw16<3>(a[13]);
-  a[6] = tw16<2>(a[6]);
-  a[10] = tw16<4>(a[10]);
-  a[14] = tw16<6>(a[14]);
-  a[7] = tw16<3>(a[7]);
-  a[11] = tw16<6>(a[11]);
-  a[15] = tw16<9>(a[15]);
-  // outer 4-point DFTs over p for each c: X[c + 4d] = sum_p V[p][c] W4^{pd}
-  dft4<false>(a[0], a[1], a[2], a[3]);
-  dft4<false>(a[4], a[5], a[6], a[7]);
-  dft4<false>(a[8], a[9], a[10], a[11]);
-  dft4<false>(a[12], a[13], a[14], a[15]);
-  // now X[c + 4d] sits at a[4c + d]: transpose the 4x4 index
-  cf b[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) b[i] = a[i];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int d = 0; d < 4; ++d) a[c + 4 * d] = b[4 * c + d];
-}
 
 // Orders LDS traffic among the lanes of one wavefront: earlier LDS writes of
 // all lanes are visible to later reads, and the compiler keeps LDS accesses
@@ -178,15 +106,13 @@ __device__ __forceinline__ void prefetch_span(const Span<S>& sp, int lane, typen
   xm1 = sp.xb[4 * lane - 1];
 }
 
-// Guarded log (src/frontend.rs:111-113) in base 2: log2(v + 2^-24).  The
-// log-mel value is this times ln 2, rounded to f32, which the
-// normalisation kernel applies as it loads the raw values (ln2_scale), so
-// the VALU-bound log-mel kernel does one operation less per value.
-// A mel value that adds nothing to the guard gives log2(2^-24) = -24
-// exactly, and -24 * f32(ln 2) rounds to f32(ln 2^-24), the reference's
-// value for digital silence.
-__device__ __forceinline__ float guarded_log2(float v) { return __log2f(v + kGuard); }
-
+// Guarded log (src/frontend.rs:111-113) in base 2: log2(v + 2^-24), where
+// the guard 2^-24 is already in v (the mel accumulators start at it).  The
+// log-mel value is this times ln 2, rounded to f32, which the normalisation
+// kernel applies as it loads the raw values (ln2_scale), so the VALU-bound
+// log-mel kernel does one operation less per value.  A mel value that adds
+// nothing to the guard gives log2(2^-24) = -24 exactly, and -24 * f32(ln 2)
+// rounds to f32(ln 2^-24), the reference's value for digital silence.
 // Raw value loaded by the normalisation kernel: RN(log2 * ln 2).
 __device__ __forceinline__ float4 ln2_scale(float4 v) {
 #pragma clang fp contract(off)  // rounded on its own, never fused into a later add
@@ -201,7 +127,7 @@ __device__ __forceinline__ float4 ln2_scale(float4 v) {
 // normalisation kernel, which works per (item, slab), reads 1 KB contiguous
 // per load instruction.
 __device__ __forceinline__ float4 log4(const f32x4& v) {
-  return make_float4(guarded_log2(v[0]), guarded_log2(v[1]), guarded_log2(v[2]), guarded_log2(v[3]));
+  return make_float4(__log2f(v[0]), __log2f(v[1]), __log2f(v[2]), __log2f(v[3]));
 }
 
 // Keeps a float4 of MFMA A operands and one of B operands allocated up to
@@ -278,14 +204,10 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     float2 tw = tb->tw256[l * 16 + k1];
     t256[k1] = {tw.x, tw.y};
   }
-  // k2 = 8 is not held: e^{-2 pi i (k + 128)/512} = -i e^{-2 pi i k/512}
-  // follows from k2 = 0 by swapping and negating parts.
-  cf t512[8];
+  // split twiddles of bins l + 16 k2, k2 < 8, as (scale, tan or cot)
+  float2 spt[8];
 #pragma unroll
-  for (int k2 = 0; k2 < 8; ++k2) {
-    float2 tw = tb->tw512[l + 16 * k2];
-    t512[k2] = {tw.x, tw.y};
-  }
+  for (int k2 = 0; k2 < 8; ++k2) spt[k2] = tb->split[l + 16 * k2];
 
   float* sb = wbuf[w];
   cf* X = reinterpret_cast<cf*>(sb) + g * kSlot;
@@ -412,20 +334,20 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
 
     // ---- 2. 512-point real FFT of frame g: lane l owns z[l + 16 m2]
     const float* fin = sb + g * kHop + 2 * l;
-    cf a[16];
+    cf zv[13];
 #pragma unroll
     for (int m2 = 0; m2 < 12; ++m2) {
       float2 v = *reinterpret_cast<const float2*>(fin + 32 * m2);
-      a[m2] = {v.x * wv[m2].x, v.y * wv[m2].y};
+      zv[m2] = {v.x, v.y};
     }
     {
       float2 v = make_float2(0.0f, 0.0f);
       if (l < 8) v = *reinterpret_cast<const float2*>(fin + 384);
-      a[12] = {v.x * wv[12].x, v.y * wv[12].y};
+      zv[12] = {v.x, v.y};
     }
-    a[13] = a[14] = a[15] = {0.0f, 0.0f};
     wave_lds_sync();  // the transpose below reuses the span's LDS
-    dft16<true>(a);
+    cf a[16];
+    dft16_windowed(zv, wv, a);  // window taps past 400 are zero
 #pragma unroll
     for (int k1 = 1; k1 < 16; ++k1) a[k1] = cmul(a[k1], t256[k1]);
 #pragma unroll
@@ -439,41 +361,35 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int m1 = 0; m1 < 16; ++m1) a[m1] = X[l * kXStride + m1];
-    dft16<false>(a);  // a[k2] = Z[l + 16 k2]
+    dft16(a);  // a[k2] = Z[l + 16 k2]
 
     // Split partner Z[256 - k] for k = l + 16 k2 lives in lane 16 - l,
     // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).
-    // 2E = A + conj B, 2O = (A - conj B) / i; X[k] = E + W O, X[256-k] = conj(E - W O);
-    // P holds 4|X|^2 (the 0.25 is folded into the filter weights).
-    // All 18 shuffles are issued before the arithmetic that consumes them.
-    cf sh[9];
+    // P holds 4|X|^2 (the 0.25 is folded into the filter weights).  Bins
+    // k2 < 8 pair k with 256 - k; bin 128 (lane 0, k2 = 8) is conj Z[128],
+    // so P[128] = 4|Z[128]|^2.  All 16 shuffles are issued before the
+    // arithmetic that consumes them.
+    cf sh[8];
 #pragma unroll
-    for (int k2 = 0; k2 < 9; ++k2) {
-      const cf src = a[(15 - k2) & 15];
+    for (int k2 = 0; k2 < 8; ++k2) {
+      const cf src = a[15 - k2];
       sh[k2] = {__shfl(src.x, partner, 16), __shfl(src.y, partner, 16)};
     }
     // The power rows overwrite the transpose slots: every lane's reads of
     // them above were issued first.
     float* P = sb + g * kPStride;
 #pragma unroll
-    for (int k2 = 0; k2 < 9; ++k2) {
+    for (int k2 = 0; k2 < 8; ++k2) {
       const cf A = a[k2];
       const cf B = (l == 0) ? a[(16 - k2) & 15] : sh[k2];
-      cf e = {A.x + B.x, A.y - B.y};
-      cf od = {A.y + B.y, B.x - A.x};
-      const cf tw = t512[k2 & 7];
-      cf t = cmul(od, k2 < 8 ? tw : cf{tw.y, -tw.x});
-      cf xp = cadd(e, t), xm = csub(e, t);
-      float pp = xp.x * xp.x + xp.y * xp.y;
-      float pm = xm.x * xm.x + xm.y * xm.y;
-      int k = l + 16 * k2;
-      if (k2 < 8) {
-        P[k] = pp;
-        P[256 - k] = pm;
-      } else if (l == 0) {
-        P[128] = pp;
-      }
+      float pp, pm;
+      if (k2 < 4) split_power<false>(A, B, spt[k2].x, spt[k2].y, pp, pm);
+      else split_power<true>(A, B, spt[k2].x, spt[k2].y, pp, pm);
+      const int k = l + 16 * k2;
+      P[k] = pp;
+      P[256 - k] = pm;
     }
+    if (l == 0) P[128] = 4.0f * fmaf(a[8].y, a[8].y, a[8].x * a[8].x);
     wave_lds_sync();
 
     // ---- 3. mel on the matrix cores: block j of chain c accumulates
@@ -482,7 +398,10 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     // operands are loaded while this group's MFMAs issue.  Chain 1 alternates
     // between two accumulators so consecutive MFMAs do not wait on each
     // other.
-    f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, c2 = c0;
+    // The guard 2^-24 of the log (src/frontend.rs:111) is added first
+    // instead of last: the accumulators start at it (chain 1's second
+    // accumulator at zero).  Digital silence still sums to exactly 2^-24.
+    f32x4 c0 = {kGuard, kGuard, kGuard, kGuard}, c1 = c0, c2 = {0.0f, 0.0f, 0.0f, 0.0f};
     float4 a1n = mel_a[kChainSteps[0] / 4][lane], b1n = *reinterpret_cast<const float4*>(pb1);
     float4 a0n = mel_a[0][lane], b0n = *reinterpret_cast<const float4*>(pb0);
 #pragma unroll
@@ -517,9 +436,14 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     pend = it.out_off + raw_frame((int64_t)(u - it.unit_off + it.q0) * kQuad);
   }
   if (pend >= 0) {
+    // the store offset computed afresh from the lane id: kept from the
+    // prologue it would stay allocated through the loop (or spill)
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int soe = 16 * (ln & 3) + 256 * (ln >> 4) + 4 * ((ln >> 2) & 3);
     float* o = out + pend;
-    *reinterpret_cast<float4*>(o + so) = log4(acc0);
-    *reinterpret_cast<float4*>(o + so + 4 * 256) = log4(acc1);
+    *reinterpret_cast<float4*>(o + soe) = log4(acc0);
+    *reinterpret_cast<float4*>(o + soe + 4 * 256) = log4(acc1);
   }
 }
 

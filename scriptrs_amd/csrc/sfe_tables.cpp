@@ -69,8 +69,10 @@ bool build_dev_tables(int sample_rate, DevTables* t) {
     // laid out per lane so the kernel indexes it affinely (l * 16 + k1)
     double a = -2.0 * M_PI * (double)((j / 16) * (j % 16)) / 256.0;
     t->tw256[j] = make_float2((float)cos(a), (float)sin(a));
-    double b = -2.0 * M_PI * (double)j / 512.0;
-    t->tw512[j] = make_float2((float)cos(b), (float)sin(b));
+  }
+  for (int k = 0; k < 128; ++k) {
+    const double b = 2.0 * M_PI * (double)k / 512.0, c = cos(b), s = sin(b);
+    t->split[k] = k < 64 ? make_float2((float)c, (float)(s / c)) : make_float2((float)s, (float)(c / s));
   }
   std::vector<float> fb((size_t)kMel * kBins);
   mel_filterbank(kNfft, kMel, sample_rate, fb.data());
