@@ -272,6 +272,20 @@ int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
  * allocated nothing. */
 int64_t sfe_debug_allocation_count(void);
 
+/* Measurement hook, no counterpart in the reference.  In a library built
+ * with -DSFE_TIMESTAMPS (python -m scriptrs_amd.build --timestamps, which
+ * writes libscriptrs_fe_ts.so; never the product library), the kernels of
+ * later launches on the current device write s_memrealtime stamps (100 MHz)
+ * into device_buf (words 64-bit words; NULL and 0 turn them off):
+ *   log-mel, per wave w = block * waves + wave, words 4w .. 4w + 3: start,
+ *   start of its first unit, end, units processed;
+ *   normalisation, per workgroup b (item * 8 + 16-feature slab), words
+ *   262144 + 4b .. + 3: start, first statistics reduced (its loads have
+ *   landed), statistics published, end.
+ * Stamps past `words` are dropped.  The product library returns
+ * SFE_INVALID_ARG. */
+int sfe_debug_stamps(void* device_buf, int64_t words);
+
 /* Turn per-kernel timing on or off for ctx.  When on, every launch of the
  * log-mel and normalisation kernels is bracketed by HIP events on the stream
  * it runs on.  Turning it on or off clears the recorded launches. */

@@ -9,7 +9,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libscriptrs_fe.so")
+# SFE_LIBRARY selects another build of the same C ABI (the measurement
+# build libscriptrs_fe_ts.so, see scriptrs_amd/stamps.py).
+LIB_PATH = os.environ.get("SFE_LIBRARY") or os.path.join(_HERE, "libscriptrs_fe.so")
 
 SFE_OK, SFE_EMPTY_AUDIO, SFE_INVALID_ARG, SFE_HIP_ERROR, SFE_AUDIO_TOO_LONG = 0, 1, 2, 3, 4
 SFE_F32, SFE_BF16 = 0, 1
@@ -22,7 +24,7 @@ EXPORTS = (
     "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_pcm",
     "sfe_extract_chunks_padded", "sfe_extract_chunks_streamed", "sfe_extract_chunks_streamed_pcm",
     "sfe_set_frame_sharing", "sfe_set_timing", "sfe_get_timing", "sfe_vad_num_windows", "sfe_vad_frames", "sfe_extract_chunks_noalloc",
-    "sfe_debug_allocation_count",
+    "sfe_debug_allocation_count", "sfe_debug_stamps",
 )
 
 
@@ -93,6 +95,7 @@ def lib() -> ctypes.CDLL:
         "sfe_set_timing": (ctypes.c_int, [vp, i32]),
         "sfe_get_timing": (ctypes.c_int, [vp, P(ctypes.c_double), P(ctypes.c_double), P(i32)]),
         "sfe_debug_allocation_count": (i64, []),
+        "sfe_debug_stamps": (ctypes.c_int, [vp, i64]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

@@ -102,26 +102,36 @@ def check_asm(src: str, extra: list[str], verbose: bool = False) -> None:
                                    "must stay a wave-uniform loop")
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(OBJ, exist_ok=True)
+LIB_TS = os.path.join(HERE, "libscriptrs_fe_ts.so")
+
+
+def build(verbose: bool = False, timestamps: bool = False) -> str:
+    """Builds the product library; with timestamps, the measurement build
+    (kernels compiled with -DSFE_TIMESTAMPS, see sfe_debug_stamps) into
+    libscriptrs_fe_ts.so instead."""
+    obj_dir = os.path.join(OBJ, "ts") if timestamps else OBJ
+    lib = LIB_TS if timestamps else LIB
+    os.makedirs(obj_dir, exist_ok=True)
     objs = []
     for src, extra in SOURCES:
-        obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+        obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
+        if timestamps and src == "sfe_kernels.hip":
+            extra = [*extra, "-DSFE_TIMESTAMPS"]
         cmd = [HIPCC, *COMMON, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
         objs.append(obj)
-        if src in MFMA_CHECKED:
+        if src in MFMA_CHECKED and not timestamps:
             check_asm(src, extra, verbose)
-    tmp = LIB + ".tmp"
+    tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timestamps="--timestamps" in sys.argv))

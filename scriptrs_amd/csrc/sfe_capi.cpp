@@ -1024,6 +1024,14 @@ int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable) {
 
 int64_t sfe_debug_allocation_count(void) { return g_allocations.load(); }
 
+int sfe_debug_stamps(void* device_buf, int64_t words) {
+  if (!sfe::stamps_built()) return fail(SFE_INVALID_ARG, "this library was built without SFE_TIMESTAMPS");
+  if (words < 0 || (!device_buf && words != 0)) return fail(SFE_INVALID_ARG, "invalid stamp buffer");
+  hipError_t e = sfe::set_stamp_buffer(device_buf, words);
+  if (e != hipSuccess) return hip_fail(e, "set_stamp_buffer");
+  return SFE_OK;
+}
+
 int sfe_set_timing(sfe_ctx* ctx, int32_t enable) {
   if (!ctx) return fail(SFE_INVALID_ARG, "null context");
   std::lock_guard<std::mutex> lock(ctx->mu);

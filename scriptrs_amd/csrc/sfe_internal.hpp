@@ -175,6 +175,10 @@ constexpr int kPcmF32 = 0;
 constexpr int kPcmI16 = 1;
 constexpr int kPcmI32 = 2;
 // Units [unit0, unit0 + n_units) in the numbering of items[].unit_off.
+// Timestamp buffer of measurement builds (-DSFE_TIMESTAMPS, sfe_kernels.hip);
+// stamps_built() is false and set_stamp_buffer fails in the product build.
+bool stamps_built();
+hipError_t set_stamp_buffer(void* buf, int64_t words);
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
                          int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
                          hipStream_t stream);

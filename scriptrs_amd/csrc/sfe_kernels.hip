@@ -29,6 +29,29 @@
 #include "sfe_pcm.hpp"
 
 namespace sfe {
+
+// Measurement builds (compiled with -DSFE_TIMESTAMPS, never the product
+// library): the kernels write s_memrealtime stamps (a 100 MHz clock shared
+// by all CUs) into a device buffer the host registers with
+// sfe_debug_stamps.  Log-mel: per wave (blockIdx * waves + wave) 4 words at
+// kStampLogmel: start, start of its first unit (end of the prologue), end,
+// units processed.  Normalisation: per workgroup 4 words at kStampNorm:
+// start, first statistics reduced (its loads have landed), statistics
+// published, end.  Every launch overwrites its region.
+#ifdef SFE_TIMESTAMPS
+constexpr int64_t kStampLogmel = 0;
+constexpr int64_t kStampNorm = 4 * 65536;
+__device__ unsigned long long* g_stamps;
+__device__ long long g_stamp_words;
+__device__ __forceinline__ void stamp(int64_t word, unsigned long long v) {
+  if (g_stamps && word < g_stamp_words) g_stamps[word] = v;
+}
+__device__ __forceinline__ unsigned long long stamp_now() { return __builtin_amdgcn_s_memrealtime(); }
+#define SFE_STAMP(word, value) stamp((word), (value))
+#else
+#define SFE_STAMP(word, value) ((void)0)
+#endif
+
 namespace {
 
 // Log-mel workgroups hold independent waves: 4 (three workgroups per CU)
@@ -155,6 +178,11 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;  // frame of this lane within the wave's 4
+#ifdef SFE_TIMESTAMPS
+  const int64_t sw = kStampLogmel + 4 * ((int64_t)blockIdx.x * NW + w);
+  if (lane == 0) SFE_STAMP(sw, stamp_now());
+  int n_done = 0;
+#endif
   const int l = lane & 15;
   const int partner = (16 - l) & 15;
 
@@ -221,7 +249,17 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   const int so = 16 * mn + 256 * (mj >> 2) + 4 * (mj & 3);
 
   const int u_first = wb + w;
-  if (u_first >= we) return;
+  if (u_first >= we) {
+#ifdef SFE_TIMESTAMPS
+    if (lane == 0) {
+      const unsigned long long t = stamp_now();
+      SFE_STAMP(sw + 1, t);
+      SFE_STAMP(sw + 2, t);
+      SFE_STAMP(sw + 3, 0ull);
+    }
+#endif
+    return;
+  }
   // The unit after the one being prefetched is taken one iteration ahead
   // (lane 0's LDS add), so its result is in by the time it is needed.
   int grab = 0;
@@ -250,8 +288,14 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
   // Raw offset (uniform) of the quad whose log-mel is held in acc0/acc1, or -1.
   int64_t pend = -1;
+#ifdef SFE_TIMESTAMPS
+  if (lane == 0) SFE_STAMP(sw + 1, stamp_now());
+#endif
 
   for (int u = u_first, un; u < we; u = un) {
+#ifdef SFE_TIMESTAMPS
+    ++n_done;
+#endif
     const Item it = it_c;
     const Span<S> sp = sp_n;
     // (for a span that is not interior nv holds stale values, decoded and
@@ -445,6 +489,12 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     *reinterpret_cast<float4*>(o + soe) = log4(acc0);
     *reinterpret_cast<float4*>(o + soe + 4 * 256) = log4(acc1);
   }
+#ifdef SFE_TIMESTAMPS
+  if (lane == 0) {
+    SFE_STAMP(sw + 2, stamp_now());
+    SFE_STAMP(sw + 3, (unsigned long long)n_done);
+  }
+#endif
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
@@ -551,23 +601,38 @@ __device__ __forceinline__ void slab_sum(double (&v)[4], double* red, int lane, 
   __syncthreads();  // red is reused by the next reduction
 }
 
-// Workgroup AND of 4 per-lane flags, same layout as slab_sum.
+// slab_sum of s together with the workgroup AND of the flags f (one LDS
+// round for both).
 template <int W, int F>
-__device__ __forceinline__ void slab_all(bool (&f)[4], int* redi, int lane, int w) {
+__device__ __forceinline__ void slab_sum_all(double (&v)[4], bool (&f)[4], double* red, int* redi, int lane, int w) {
   constexpr int L = F / 4;
   unsigned m = 0;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) m |= (f[c] ? 1u : 0u) << c;
+  for (int c = 0; c < 4; ++c) {
+    v[c] = group_sum<L>(v[c]);
+    m |= (f[c] ? 1u : 0u) << c;
+  }
 #pragma unroll
   for (int off = L; off < 64; off <<= 1) m &= __shfl_xor(m, off, 64);
-  if (lane < L) redi[w * L + lane] = (int)m;
+  if (lane < L) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[w * F + 4 * lane + c] = v[c];
+    redi[w * L + lane] = (int)m;
+  }
   __syncthreads();
+  const int q = lane % L;
   unsigned t = 0xfu;
 #pragma unroll
-  for (int u = 0; u < W; ++u) t &= (unsigned)redi[u * L + lane % L];
+  for (int u = 0; u < W; ++u) t &= (unsigned)redi[u * L + q];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) f[c] = (t >> c) & 1u;
-  __syncthreads();
+  for (int c = 0; c < 4; ++c) {
+    double a = 0.0;
+#pragma unroll
+    for (int u = 0; u < W; ++u) a += red[u * F + 4 * q + c];
+    v[c] = a;
+    f[c] = (t >> c) & 1u;
+  }
+  __syncthreads();  // red is reused by the next reduction
 }
 
 // (x - mean) / sd, correctly rounded, from r = RN(1 / sd): q = RN(d r) is
@@ -580,27 +645,32 @@ __device__ __forceinline__ float norm_div(float x, float mean, float sd, float r
   return __fmaf_rn(__fmaf_rn(-sd, q, d), r, q);
 }
 
-// s holds sums of (x - x0), q sums of squared deviations from the f32 mean.
-// Per-feature (mean, sd, 1/sd) of the slab, published in LDS by the lanes
-// that own each feature (wave 0, lanes 0 .. F / 4 - 1) for the store phase.
+// s holds sums of (x - x0) (x0 the feature's first value), q sums of
+// squared deviations from the f32 mean, both reduced over the item.
+// Per-feature (mean, sd, 1/sd) of the slab, published in LDS for the store
+// phase by wave 0's lanes 0 .. F - 1, one feature each (lane i: feature
+// 4 (i % (F / 4)) + i / (F / 4), whose totals it holds).
 template <int F>
 __device__ __forceinline__ void publish_stats(const double (&s)[4], const double (&q)[4], const bool (&cst)[4],
                                               const float4& x0, int T, int lane, int w, float* st) {
-  if (w == 0 && lane < F / 4) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float mean, sd;
-      if (cst[c]) {
-        constant_row_stats(comp(x0, c), T, &mean, &sd);
-      } else {
-        mean = (float)((double)comp(x0, c) + s[c] / (double)T);
-        sd = __fadd_rn(__fsqrt_rn((float)(q[c] / (double)(T - 1))), 1e-5f);
-      }
-      const int f = 4 * lane + c;
-      st[3 * f] = mean;
-      st[3 * f + 1] = sd;
-      st[3 * f + 2] = __fdiv_rn(1.0f, sd);
+  constexpr int L = F / 4;
+  if (w == 0 && lane < F) {
+    const int c = lane / L;
+    const int f = 4 * (lane % L) + c;
+    const double S = c == 0 ? s[0] : (c == 1 ? s[1] : (c == 2 ? s[2] : s[3]));
+    const double Q = c == 0 ? q[0] : (c == 1 ? q[1] : (c == 2 ? q[2] : q[3]));
+    const bool k = c == 0 ? cst[0] : (c == 1 ? cst[1] : (c == 2 ? cst[2] : cst[3]));
+    const float xf = comp(x0, c);
+    float mean, sd;
+    if (k) {
+      constant_row_stats(xf, T, &mean, &sd);
+    } else {
+      mean = (float)((double)xf + S / (double)T);
+      sd = __fadd_rn(__fsqrt_rn((float)(Q / (double)(T - 1))), 1e-5f);
     }
+    st[3 * f] = mean;
+    st[3 * f + 1] = sd;
+    st[3 * f + 2] = __fdiv_rn(1.0f, sd);
   }
   __syncthreads();
 }
@@ -681,6 +751,10 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   __shared__ __align__(16) float tb[F * S::kTStride];
   const int item = work / S::kSlabs;
   if (item >= n_items) return;
+#ifdef SFE_TIMESTAMPS
+  const int64_t sn = kStampNorm + 4 * (int64_t)work;
+  if (threadIdx.x == 0) SFE_STAMP(sn, stamp_now());
+#endif
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int q = lane % S::kLanesPerFrame;
@@ -789,8 +863,10 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
           }
         }
       }
-      slab_sum<W, F>(s, red, lane, w);
-      slab_all<W, F>(eq, redi, lane, w);
+      slab_sum_all<W, F>(s, eq, red, redi, lane, w);
+#ifdef SFE_TIMESTAMPS
+      if (threadIdx.x == 0) SFE_STAMP(sn + 1, stamp_now());
+#endif
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const float m = (float)((double)comp(x0, c) + s[c] / (double)T);
@@ -830,6 +906,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
       }
       slab_sum<W, F>(sq, red, lane, w);
       publish_stats<F>(s, sq, eq, x0, T, lane, w, st);
+#ifdef SFE_TIMESTAMPS
+      if (threadIdx.x == 0) SFE_STAMP(sn + 2, stamp_now());
+#endif
       const int chunks = (T + kChunk - 1) / kChunk;
 #pragma unroll
       for (int ch = 0; ch < (N + X) / 4; ++ch) {
@@ -846,6 +925,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
           __syncthreads();
         }
       }
+#ifdef SFE_TIMESTAMPS
+      if (threadIdx.x == 0) SFE_STAMP(sn + 3, stamp_now());
+#endif
       return;
     }
   }
@@ -873,8 +955,10 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
       s[c] += (double)a;
     }
   }
-  slab_sum<W, F>(s, red, lane, w);
-  slab_all<W, F>(eq, redi, lane, w);
+  slab_sum_all<W, F>(s, eq, red, redi, lane, w);
+#ifdef SFE_TIMESTAMPS
+  if (threadIdx.x == 0) SFE_STAMP(sn + 1, stamp_now());
+#endif
   float m[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) m[c] = (float)((double)comp(x0, c) + s[c] / (double)T);
@@ -898,6 +982,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   }
   slab_sum<W, F>(sq, red, lane, w);
   publish_stats<F>(s, sq, eq, x0, T, lane, w, st);
+#ifdef SFE_TIMESTAMPS
+  if (threadIdx.x == 0) SFE_STAMP(sn + 2, stamp_now());
+#endif
   const int chunks = (T + kChunk - 1) / kChunk;
   for (int ch = 0; ch < chunks; ++ch) {
     float4 e[4];
@@ -914,6 +1001,9 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
     store_chunk<W, F>(tb, st, kChunk * ch, T, rs, lane, w, ob);
     __syncthreads();
   }
+#ifdef SFE_TIMESTAMPS
+  if (threadIdx.x == 0) SFE_STAMP(sn + 3, stamp_now());
+#endif
 }
 
 // Workgroups of kNormMainWaves waves over 16-feature slabs, three per CU;
@@ -944,6 +1034,28 @@ __global__ __launch_bounds__(64 * kNormWideWaves) void sfe_norm_wide_kernel(cons
 }
 
 }  // namespace
+
+bool stamps_built() {
+#ifdef SFE_TIMESTAMPS
+  return true;
+#else
+  return false;
+#endif
+}
+
+hipError_t set_stamp_buffer(void* buf, int64_t words) {
+#ifdef SFE_TIMESTAMPS
+  unsigned long long* p = static_cast<unsigned long long*>(buf);
+  long long n = words;
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_stamps), &p, sizeof(p));
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_stamp_words), &n, sizeof(n));
+  return e;
+#else
+  (void)buf;
+  (void)words;
+  return hipErrorNotSupported;
+#endif
+}
 
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
 int64_t units_for(int64_t T) { return (T + kQuad - 1) / kQuad; }
