@@ -76,6 +76,7 @@ def summarize(st: np.ndarray) -> dict:
             "wave_end_us": {"p10": pct(end * us, 10), "p50": pct(end * us, 50), "p90": pct(end * us, 90),
                             "max": float(end.max() * us)},
             "units_per_wave": {"min": int(units.min()), "p50": pct(units, 50), "max": int(units.max())},
+            "units_total": int(units.sum()),
             "us_per_unit": {"p10": pct(per_unit, 10), "p50": pct(per_unit, 50), "p90": pct(per_unit, 90)},
         }
     if len(nm):

@@ -31,6 +31,23 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.EXPORTS)
 
 
+def test_product_library_has_no_stamps():
+    """sfe_debug_stamps is only live in the measurement build; the product
+    library refuses it without touching the device."""
+    L = _lib.lib()
+    assert L.sfe_debug_stamps(None, 0) == _lib.SFE_INVALID_ARG
+    assert "SFE_TIMESTAMPS" in _lib.last_error()
+
+
+def test_measurement_build_exports_the_same_abi():
+    from scriptrs_amd import stamps
+    if not os.path.exists(stamps.TS_LIB):
+        pytest.skip("measurement build not present")
+    T = ctypes.CDLL(stamps.TS_LIB)
+    for n in header_functions():
+        assert hasattr(T, n), n
+
+
 def test_config_defaults_match_reference():
     c = _lib.SfeConfig()
     _lib.lib().sfe_config_default(ctypes.byref(c))

@@ -11,8 +11,11 @@ use them.
   task over the whole recording (src/long_form.rs:161-163); a longer one is
   planned and every task is featurized, in task order, with the frame
   offsets of the oracle's planner and values against the oracle.
+* The measurement build's stamps (scriptrs_amd/stamps.py) are consistent.
 """
 import ctypes
+import json
+import os
 
 import numpy as np
 import pytest
@@ -24,6 +27,7 @@ from oracle import planner
 from scriptrs_amd import (AudioTooLong, ChunkPreparer, TranscriptionConfig, _lib, featurize_long_form, synth)
 
 pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _flush(msg):
@@ -117,3 +121,24 @@ def test_featurize_long_form_planned_branch(preparer, n):
             for t in planner.build_fast_execution_plan(n)]
     assert len(want) >= 2
     _check_long_form(lf, rec, want)
+
+
+def test_measurement_build_stamps_are_consistent():
+    """The measurement build's timelines (scriptrs_amd/stamps.py) on the
+    config-1 clip: every log-mel wave and normalisation workgroup left
+    ordered stamps, and the waves' units add up to the launch's quads."""
+    import subprocess
+    import sys
+    from scriptrs_amd import stamps
+    if not os.path.exists(stamps.TS_LIB):
+        pytest.skip("measurement build not present (python -m scriptrs_amd.build --timestamps)")
+    _flush("case: measurement build stamps, config 1")
+    r = subprocess.run([sys.executable, "-m", "scriptrs_amd.stamps", "--workload", "config1", "--warmup", "3"],
+                       capture_output=True, text=True, timeout=300, cwd=ROOT)
+    assert r.returncode == 0, r.stdout + r.stderr
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    lm, nm = res["logmel"], res["norm"]
+    assert lm["waves"] > 0 and lm["span_us"] > 0 and lm["prologue_us"]["p50"] >= 0
+    assert lm["units_total"] == (1001 + 3) // 4
+    assert nm["workgroups"] == 8 and nm["span_us"] > 0
+    assert nm["lifetime_us"]["p50"] >= nm["stores_us"]["p50"] >= 0
