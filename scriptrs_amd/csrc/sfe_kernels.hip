@@ -179,8 +179,9 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;  // frame of this lane within the wave's 4
 #ifdef SFE_TIMESTAMPS
-  const int64_t sw = kStampLogmel + 4 * ((int64_t)blockIdx.x * NW + w);
-  if (lane == 0) SFE_STAMP(sw, stamp_now());
+  // (the word index is recomputed where used: kept live it cost a register)
+#define SFE_LOGMEL_WORD (kStampLogmel + 4 * ((int64_t)blockIdx.x * NW + w))
+  if (lane == 0) SFE_STAMP(SFE_LOGMEL_WORD, stamp_now());
   int n_done = 0;
 #endif
   const int l = lane & 15;
@@ -253,9 +254,9 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
 #ifdef SFE_TIMESTAMPS
     if (lane == 0) {
       const unsigned long long t = stamp_now();
-      SFE_STAMP(sw + 1, t);
-      SFE_STAMP(sw + 2, t);
-      SFE_STAMP(sw + 3, 0ull);
+      SFE_STAMP(SFE_LOGMEL_WORD + 1, t);
+      SFE_STAMP(SFE_LOGMEL_WORD + 2, t);
+      SFE_STAMP(SFE_LOGMEL_WORD + 3, 0ull);
     }
 #endif
     return;
@@ -288,13 +289,12 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
   // Raw offset (uniform) of the quad whose log-mel is held in acc0/acc1, or -1.
   int64_t pend = -1;
-#ifdef SFE_TIMESTAMPS
-  if (lane == 0) SFE_STAMP(sw + 1, stamp_now());
-#endif
 
   for (int u = u_first, un; u < we; u = un) {
 #ifdef SFE_TIMESTAMPS
-    ++n_done;
+    // (stamped here rather than before the loop: there it cost a register)
+    if (n_done == 0 && lane == 0) SFE_STAMP(SFE_LOGMEL_WORD + 1, stamp_now());
+    n_done = __builtin_amdgcn_readfirstlane(n_done) + 1;
 #endif
     const Item it = it_c;
     const Span<S> sp = sp_n;
@@ -491,8 +491,8 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   }
 #ifdef SFE_TIMESTAMPS
   if (lane == 0) {
-    SFE_STAMP(sw + 2, stamp_now());
-    SFE_STAMP(sw + 3, (unsigned long long)n_done);
+    SFE_STAMP(SFE_LOGMEL_WORD + 2, stamp_now());
+    SFE_STAMP(SFE_LOGMEL_WORD + 3, (unsigned long long)__builtin_amdgcn_readfirstlane(n_done));
   }
 #endif
 }
