@@ -277,10 +277,10 @@ int64_t sfe_debug_allocation_count(void);
  * writes libscriptrs_fe_ts.so; never the product library), the kernels of
  * later launches on the current device write s_memrealtime stamps (100 MHz)
  * into device_buf (words 64-bit words; NULL and 0 turn them off):
- *   log-mel, per wave w = block * waves + wave, words 4w .. 4w + 3: start,
- *   start of its first unit, end, units processed;
+ *   log-mel, per wave w = block * waves + wave, words 8w .. 8w + 5: start,
+ *   loop entry, end, units processed, (unused), item descriptors loaded;
  *   normalisation, per workgroup b (item * 8 + 16-feature slab), words
- *   262144 + 4b .. + 3: start, first statistics reduced (its loads have
+ *   524288 + 4b .. + 3: start, first statistics reduced (its loads have
  *   landed), statistics published, end.
  * Stamps past `words` are dropped.  The product library returns
  * SFE_INVALID_ARG. */

@@ -82,6 +82,14 @@ def lane_masked_loops(asm: str, kernel: str) -> int:
 LANE_LOOP_LIMITS = {"sfe_logmel_kernelI[fsi]Li12E": 0, "sfe_logmel_kernelI[fsi]Li4E": 1}
 
 
+def vgpr_spills(asm: str) -> dict[str, int]:
+    """Kernel name -> .vgpr_spill_count from the code object metadata."""
+    out = {}
+    for m in re.finditer(r"\.name:\s+(\S+)\n(?:(?!\.name:).)*?\.vgpr_spill_count:\s+(\d+)", asm, re.S):
+        out[m.group(1)] = int(m.group(2))
+    return out
+
+
 def check_asm(src: str, extra: list[str], verbose: bool = False) -> None:
     with tempfile.TemporaryDirectory() as tmp:
         out = os.path.join(tmp, "k.s")
@@ -93,6 +101,11 @@ def check_asm(src: str, extra: list[str], verbose: bool = False) -> None:
     bad = mfma_operand_overlaps(asm)
     if bad:
         raise RuntimeError(f"{src}: MFMA destination overlaps its own A/B operand:\n  " + "\n  ".join(bad))
+    # A spill in these kernels puts scratch loads (and full vmcnt waits) into
+    # their loops: the product and the measurement build must have none.
+    spilled = {k: n for k, n in vgpr_spills(asm).items() if n and ("logmel" in k or "norm" in k)}
+    if spilled:
+        raise RuntimeError(f"{src}: registers spilled in " + ", ".join(f"{k} ({n})" for k, n in spilled.items()))
     for pat, limit in LANE_LOOP_LIMITS.items():
         for t in "fsi":
             k = pat.replace("[fsi]", t)
@@ -122,7 +135,7 @@ def build(verbose: bool = False, timestamps: bool = False) -> str:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
         objs.append(obj)
-        if src in MFMA_CHECKED and not timestamps:
+        if src in MFMA_CHECKED:
             check_asm(src, extra, verbose)
     tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

@@ -302,7 +302,8 @@ enum Stages { kLogmel = 1, kNorm = 2, kBoth = 3 };
 
 int launch_pair(sfe_ctx* ctx, const Source& src, const Item* lm, const Item* d_lm, int n_lm, const Item* norm,
                 const Item* d_norm, int n_norm, float* raw, void* out, int32_t out_dtype, int pad_to,
-                hipStream_t stream, int stages = kBoth, bool allow_timing = true) {
+                hipStream_t stream, int stages = kBoth, bool allow_timing = true,
+                const int32_t* d_wave_item = nullptr) {
   if (n_lm <= 0 && n_norm <= 0) return SFE_OK;
   const int u0 = n_lm > 0 ? lm[0].unit_off : 0;
   const int u1 = n_lm > 0 ? lm[n_lm - 1].unit_off + lm[n_lm - 1].n_units : 0;
@@ -315,7 +316,7 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* lm, const Item* d_l
   if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
   if (stages & kLogmel)
     SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_lm, n_lm, u0, u1 - u0, ctx->d_tables,
-                               ctx->cfg.preemphasis, raw, ctx->cus, stream));
+                               ctx->cfg.preemphasis, raw, ctx->cus, d_wave_item, stream));
   if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
   if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
   if (stages & kNorm)
@@ -330,6 +331,24 @@ int launch_own(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d
                int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth, bool allow_timing = true) {
   return launch_pair(ctx, src, items, d_items, n, items, d_items, n, raw, out, out_dtype, pad_to, stream, stages,
                      allow_timing);
+}
+
+// The log-mel launch over table[0, n_lm): its grid, and whether its
+// first-item table (sfe::logmel_wave_items) fits kMaxLogmelWaves entries.
+struct WaveTable {
+  sfe::LogmelGrid grid{0, 0};
+  int u0 = 0, n_units = 0;
+  size_t entries = 0;  // 0: the kernel searches instead
+};
+WaveTable wave_table(const Item* lm, size_t n_lm, int cus) {
+  WaveTable t;
+  if (n_lm == 0) return t;
+  t.u0 = lm[0].unit_off;
+  t.n_units = lm[n_lm - 1].unit_off + lm[n_lm - 1].n_units - t.u0;
+  t.grid = sfe::logmel_grid(t.n_units, cus);
+  const size_t n = (size_t)t.grid.waves * t.grid.blocks;
+  if (t.n_units > 0 && n <= (size_t)sfe::kMaxLogmelWaves) t.entries = n;
+  return t;
 }
 
 // Uploads items through the pinned staging buffer on `stream`, then runs
@@ -356,27 +375,36 @@ int run_items(sfe_ctx* ctx, const Source& src, const std::vector<Item>& items, i
   const std::vector<Item>& table = ctx->plan_table;
   const size_t n_lm = ctx->plan_n_lm;
   const int64_t total_tiles = ctx->plan_tiles;
-  const size_t mbytes = table.size() * sizeof(Item);
+  // The upload: the table, then the log-mel launch's first-item table.
+  const size_t tbytes = table.size() * sizeof(Item);
+  const WaveTable wt = wave_table(table.data(), n_lm, ctx->cus);
+  const size_t mbytes = tbytes + wt.entries * sizeof(int32_t);
   // A call with the same table as the previous upload (repeated plans,
-  // equal-sized windows) reuses the device copy.  The table is only read by
-  // the kernels, so earlier work still in flight is unaffected.
+  // equal-sized windows) reuses the device copy (the first-item table
+  // follows from the table).  The table is only read by the kernels, so
+  // earlier work still in flight is unaffected.
   const bool same = ctx->meta.ptr && ctx->meta_items.size() == table.size() &&
-                    memcmp(ctx->meta_items.data(), table.data(), mbytes) == 0;
+                    memcmp(ctx->meta_items.data(), table.data(), tbytes) == 0;
   if (!same) {
     ctx->meta_items.clear();
     SFE_HIP(ctx->h_meta.reserve(mbytes));
     SFE_HIP(ctx->meta.reserve(mbytes));
-    memcpy(ctx->h_meta.ptr, table.data(), mbytes);
+    memcpy(ctx->h_meta.ptr, table.data(), tbytes);
+    if (wt.entries)
+      sfe::logmel_wave_items(table.data(), (int)n_lm, wt.u0, wt.n_units, wt.grid,
+                             reinterpret_cast<int32_t*>(static_cast<char*>(ctx->h_meta.ptr) + tbytes));
     SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, stream));
     SFE_HIP(hipEventRecord(ctx->h_meta.ev, stream));
     ctx->h_meta.pending = true;
     ctx->meta_items = table;
   }
   const Item* d_table = static_cast<const Item*>(ctx->meta.ptr);
+  const int32_t* d_wave =
+      wt.entries ? reinterpret_cast<const int32_t*>(static_cast<const char*>(ctx->meta.ptr) + tbytes) : nullptr;
   SFE_HIP(ctx->scratch.reserve((size_t)total_tiles * sfe::kRawTile * sizeof(float)));
   float* raw = static_cast<float*>(ctx->scratch.ptr);
   const int rc = launch_pair(ctx, src, table.data(), d_table, (int)n_lm, table.data() + n_lm, d_table + n_lm,
-                             (int)items.size(), raw, out, out_dtype, pad_to, stream);
+                             (int)items.size(), raw, out, out_dtype, pad_to, stream, kBoth, true, d_wave);
   if (rc) return rc;
   SFE_HIP(mark_last(ctx, stream));
   return SFE_OK;
@@ -774,7 +802,8 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     SFE_HIP(sfe::noalloc_lock(ctx->device, &dev_lock));
     std::lock_guard<std::mutex> lock(ctx->mu);
     const size_t entries = (size_t)(sfe::kPlanEntriesPerItem + 1) * n;
-    if (!ctx->noalloc || ctx->h_meta.cap < entries * sizeof(Item) || ctx->na_in.capacity() < (size_t)n)
+    if (!ctx->noalloc || ctx->h_meta.cap < entries * sizeof(Item) + sfe::kMaxLogmelWaves * sizeof(int32_t) ||
+        ctx->na_in.capacity() < (size_t)n)
       return fail(SFE_HIP_ERROR, "context has no static scratch");
     int64_t fo = 0, own_tiles = 0;
     frame_offsets[0] = 0;
@@ -799,11 +828,20 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     SFE_HIP(sfe::noalloc_order(ctx->device, s));
     Item* d_table = reinterpret_cast<Item*>(ctx->noalloc);
     float* raw = reinterpret_cast<float*>(ctx->noalloc + sfe::kNoAllocItemBytes);
-    SFE_HIP(hipMemcpyAsync(d_table, table, (n_lm + n) * sizeof(Item), hipMemcpyHostToDevice, s));
+    // the table, then the log-mel launch's first-item table, in one copy
+    // (the item region holds kMaxLogmelWaves entries past the largest table)
+    const size_t tbytes = (n_lm + n) * sizeof(Item);
+    const WaveTable wt = wave_table(table, n_lm, ctx->cus);
+    if (wt.entries)
+      sfe::logmel_wave_items(table, (int)n_lm, wt.u0, wt.n_units, wt.grid,
+                             reinterpret_cast<int32_t*>(reinterpret_cast<char*>(table) + tbytes));
+    const int32_t* d_wave =
+        wt.entries ? reinterpret_cast<const int32_t*>(ctx->noalloc + tbytes) : nullptr;
+    SFE_HIP(hipMemcpyAsync(d_table, table, tbytes + wt.entries * sizeof(int32_t), hipMemcpyHostToDevice, s));
     SFE_HIP(hipEventRecord(ctx->h_meta.ev, s));
     ctx->h_meta.pending = true;
     rc = launch_pair(ctx, f32_source(recording), table, d_table, (int)n_lm, table + n_lm, d_table + n_lm, n, raw, out,
-                     out_dtype, 0, s, kBoth, false);
+                     out_dtype, 0, s, kBoth, false, d_wave);
     if (rc) return rc;
     SFE_HIP(mark_last(ctx, s));
     SFE_HIP(sfe::noalloc_mark(ctx->device, s));

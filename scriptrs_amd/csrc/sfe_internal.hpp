@@ -179,10 +179,55 @@ constexpr int kPcmI32 = 2;
 // stamps_built() is false and set_stamp_buffer fails in the product build.
 bool stamps_built();
 hipError_t set_stamp_buffer(void* buf, int64_t words);
+constexpr int kLogmelWavesPerSimd = 3;
+// Log-mel launch shape: launches with at least 4 units per wave on every
+// CU's 12 waves take one 12-wave workgroup per CU; smaller ones 4-wave
+// workgroups, up to 3 per CU, each wave taking at least one unit.
+constexpr int kLogmelWavesSmall = 4;
+constexpr int kLogmelWavesBig = 12;
+struct LogmelGrid {
+  int waves;   // per workgroup
+  int blocks;  // workgroups
+};
+inline LogmelGrid logmel_grid(int n_units, int cus) {
+  if ((int64_t)n_units >= (int64_t)4 * kLogmelWavesBig * cus) {
+    const int want = (n_units + kLogmelWavesBig - 1) / kLogmelWavesBig;
+    return {kLogmelWavesBig, want < cus ? want : cus};
+  }
+  const int want = (n_units + kLogmelWavesSmall - 1) / kLogmelWavesSmall;
+  const int cap = kLogmelWavesPerSimd * cus;
+  return {kLogmelWavesSmall, want < cap ? want : cap};
+}
+// Units [*wb, *we) of workgroup b of G workgroups of NW waves, over units
+// [unit0, unit0 + n_units).  4-wave grids run 3 workgroups per CU, dispatched
+// a CU slot at a time, and a SIMD issues its oldest wave first, so the later
+// slots run slower: their shares are weighted 11 : 10 : 9 by slot (blocks in
+// thirds of the grid) when every wave has at least 8 units.  The log-mel
+// kernel and the host's first-item table (logmel_wave_items) both use this.
+__host__ __device__ inline void logmel_share(int64_t G, int64_t b, int NW, int unit0, int n_units, int* wb, int* we) {
+  const int64_t B1 = G / 3, B2 = 2 * G / 3;
+  const bool weighted = NW == kLogmelWavesSmall && G >= 3 && (int64_t)n_units >= (int64_t)8 * NW * G;
+  auto cum = [=](int64_t c) -> int64_t {  // share of the blocks before block c
+    if (!weighted) return c;
+    const int64_t c1 = c < B1 ? c : B1, c2 = c < B1 ? 0 : (c < B2 ? c - B1 : B2 - B1), c3 = c > B2 ? c - B2 : 0;
+    return 11 * c1 + 10 * c2 + 9 * c3;
+  };
+  const int64_t tot = cum(G);
+  *wb = unit0 + (int)((int64_t)n_units * cum(b) / tot);
+  *we = unit0 + (int)((int64_t)n_units * cum(b + 1) / tot);
+}
+// Item of each wave's first unit, for a launch of grid g over units
+// [unit0, unit0 + n_units) of items[0, n_items) (sorted by unit_off):
+// out[b * g.waves + w] = the last item whose unit_off <= wb + w (0 for a wave
+// with no unit).  The kernel then skips its item search, a chain of
+// dependent loads at the start of every wave.  At most kMaxLogmelWaves
+// entries; larger grids go without (the kernel searches).
+constexpr int kMaxLogmelWaves = 4096;
+void logmel_wave_items(const Item* items, int n_items, int unit0, int n_units, LogmelGrid g, int32_t* out);
+// wave_item: the table above on the device for this launch, or null.
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
                          int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
-                         hipStream_t stream);
-constexpr int kLogmelWavesPerSimd = 3;
+                         const int32_t* wave_item, hipStream_t stream);
 // Normalises raw (f32 log2 values in 16-frame tiles, see Item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias
 // raw) or bf16 (uint16_t*) when out_bf16 is set.  max_T: the longest item's
@@ -198,7 +243,8 @@ constexpr int kNoAllocMaxItems = 4096;
 // (a plan has at most kPlanEntriesPerItem log-mel entries and one
 // normalisation entry per item)
 constexpr size_t kNoAllocItemBytes =
-    ((size_t)(kPlanEntriesPerItem + 1) * kNoAllocMaxItems * sizeof(Item) + 255) / 256 * 256;
+    ((size_t)(kPlanEntriesPerItem + 1) * kNoAllocMaxItems * sizeof(Item) + kMaxLogmelWaves * sizeof(int32_t) +
+     255) / 256 * 256;
 constexpr size_t kNoAllocRawBytes = (size_t)64 << 20;
 // Device address of this device's static scratch (looked up once per device).
 hipError_t noalloc_scratch(int device, void** out);

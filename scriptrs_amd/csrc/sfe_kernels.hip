@@ -33,14 +33,16 @@ namespace sfe {
 // Measurement builds (compiled with -DSFE_TIMESTAMPS, never the product
 // library): the kernels write s_memrealtime stamps (a 100 MHz clock shared
 // by all CUs) into a device buffer the host registers with
-// sfe_debug_stamps.  Log-mel: per wave (blockIdx * waves + wave) 4 words at
-// kStampLogmel: start, start of its first unit (end of the prologue), end,
-// units processed.  Normalisation: per workgroup 4 words at kStampNorm:
-// start, first statistics reduced (its loads have landed), statistics
-// published, end.  Every launch overwrites its region.
+// sfe_debug_stamps.  Log-mel: per wave (blockIdx * waves + wave) 8 words at
+// kStampLogmel: start, loop entry (end of the prologue), end, units
+// processed, (unused), item descriptors loaded (after their first use).
+// (A stamp after the workgroup barrier of the mel table made the compiler
+// spill 42 registers in the main loop, so there is none.)  Normalisation: per workgroup 4 words at kStampNorm: start,
+// first statistics reduced (its loads have landed), statistics published,
+// end.  Every launch overwrites its region.
 #ifdef SFE_TIMESTAMPS
 constexpr int64_t kStampLogmel = 0;
-constexpr int64_t kStampNorm = 4 * 65536;
+constexpr int64_t kStampNorm = 8 * 65536;
 __device__ unsigned long long* g_stamps;
 __device__ long long g_stamp_words;
 __device__ __forceinline__ void stamp(int64_t word, unsigned long long v) {
@@ -57,8 +59,8 @@ namespace {
 // Log-mel workgroups hold independent waves: 4 (three workgroups per CU)
 // for launches that do not fill the machine, 12 (one per CU, all of its
 // waves sharing one work counter) for those that do.
-constexpr int kWavesSmall = 4;
-constexpr int kWavesBig = 12;
+constexpr int kWavesSmall = kLogmelWavesSmall;
+constexpr int kWavesBig = kLogmelWavesBig;
 constexpr int kXStride = 17;                         // transpose row stride (complex)
 constexpr int kSlot = 16 * kXStride;                 // complex per frame slot
 constexpr float kGuard = 5.9604644775390625e-08f;    // 2^-24, src/frontend.rs:111
@@ -168,7 +170,8 @@ __device__ __forceinline__ void mfma_keep(const float4& a, const float4& b) {
 template <typename S, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kLogmelWavesPerSimd, kLogmelWavesPerSimd)))
 void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ items, int n_items, int unit0,
-                       int n_units, const DevTables* __restrict__ tb, float coef, Decode dc, float* __restrict__ out) {
+                       int n_units, const DevTables* __restrict__ tb, float coef, Decode dc, float* __restrict__ out,
+                       const int32_t* __restrict__ wave_item) {
   constexpr int kWaves = NW;
   constexpr int kThreads = 64 * NW;
   __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
@@ -180,7 +183,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   const int g = lane >> 4;  // frame of this lane within the wave's 4
 #ifdef SFE_TIMESTAMPS
   // (the word index is recomputed where used: kept live it cost a register)
-#define SFE_LOGMEL_WORD (kStampLogmel + 4 * ((int64_t)blockIdx.x * NW + w))
+#define SFE_LOGMEL_WORD (kStampLogmel + 8 * ((int64_t)blockIdx.x * NW + w))
   if (lane == 0) SFE_STAMP(SFE_LOGMEL_WORD, stamp_now());
   int n_done = 0;
 #endif
@@ -188,28 +191,13 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   const int partner = (16 - l) & 15;
 
   // Work: workgroup b owns units [wb, we) of this launch's [unit0, unit0 +
-  // n_units) (items[].unit_off counts in the same numbering), and its waves
-  // take them one at a time through an LDS counter, so a wave that gets less
-  // issue on its SIMD takes fewer units.  With 4-wave workgroups the
-  // persistent grid is 3 workgroups per CU, dispatched a CU slot at a time;
-  // a SIMD issues its oldest wave first, so the later slots run slower, and
-  // with equal shares they finished 20 us after the first (1 h workload).
-  // Their shares are then weighted 11 : 10 : 9 by slot (blocks in thirds of
-  // the grid) when every wave has at least 8 units.
+  // n_units) (items[].unit_off counts in the same numbering; logmel_share,
+  // which weights 4-wave grids' slots), and its waves take them one at a
+  // time through an LDS counter, so a wave that gets less issue on its SIMD
+  // takes fewer units.
   __shared__ int wg_next;
   int wb, we;
-  {
-    const int64_t G = gridDim.x, b = blockIdx.x, B1 = G / 3, B2 = 2 * G / 3;
-    const bool weighted = NW == kWavesSmall && G >= 3 && (int64_t)n_units >= 8 * kWaves * G;
-    auto cum = [=](int64_t c) -> int64_t {  // share of the blocks before block c
-      if (!weighted) return c;
-      const int64_t c1 = c < B1 ? c : B1, c2 = c < B1 ? 0 : (c < B2 ? c - B1 : B2 - B1), c3 = c > B2 ? c - B2 : 0;
-      return 11 * c1 + 10 * c2 + 9 * c3;
-    };
-    const int64_t tot = cum(G);
-    wb = unit0 + (int)((int64_t)n_units * cum(b) / tot);
-    we = unit0 + (int)((int64_t)n_units * cum(b + 1) / tot);
-  }
+  logmel_share(gridDim.x, blockIdx.x, NW, unit0, n_units, &wb, &we);
   if (tid == 0) wg_next = wb + kWaves;  // each wave's first unit is wb + w
 
   // A operands of the mel MFMAs, shared by the workgroup's waves.
@@ -269,7 +257,9 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   // being prefetched, it_n the item after it, loaded one item ahead so an
   // item boundary never waits on memory.  Every item spans at least one unit.
   int li = 0;
-  {
+  if (wave_item) {
+    li = wave_item[(int64_t)blockIdx.x * NW + w];  // from the host (logmel_wave_items)
+  } else {
     int hi = n_items - 1;
     while (li < hi) {
       int mid = (li + hi + 1) >> 1;
@@ -282,6 +272,10 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   // The samples of unit u + 1 are loaded into registers while unit u is
   // transformed, so the global-load latency hides behind the FFT.
   Span<S> sp_n = make_span(it_c, samples, u_first);
+#ifdef SFE_TIMESTAMPS
+  // (after the first use of the item descriptor, which waits for it)
+  if (lane == 0) SFE_STAMP(SFE_LOGMEL_WORD + 5, stamp_now());
+#endif
   typename Pcm<S>::V4 nv[kSpanVec] = {};
   S nxm1 = 0;
   prefetch_span(sp_n, lane, nv, nxm1);
@@ -1063,38 +1057,51 @@ int64_t units_for(int64_t T) { return (T + kQuad - 1) / kQuad; }
 template <int NW>
 hipError_t launch_logmel_t(const void* samples, int pcm, const Decode& dc, const Item* items, int n_items, int unit0,
                            int n_units, const DevTables* tables, float preemph, float* raw_out, int grid,
-                           hipStream_t stream) {
+                           const int32_t* wave_item, hipStream_t stream) {
   const dim3 g(grid), b(64 * NW);
   if (pcm == kPcmI16)
     sfe_logmel_kernel<int16_t, NW><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items, unit0,
-                                                        n_units, tables, preemph, dc, raw_out);
+                                                        n_units, tables, preemph, dc, raw_out, wave_item);
   else if (pcm == kPcmI32)
     sfe_logmel_kernel<int32_t, NW><<<g, b, 0, stream>>>(static_cast<const int32_t*>(samples), items, n_items, unit0,
-                                                        n_units, tables, preemph, dc, raw_out);
+                                                        n_units, tables, preemph, dc, raw_out, wave_item);
   else
     sfe_logmel_kernel<float, NW><<<g, b, 0, stream>>>(static_cast<const float*>(samples), items, n_items, unit0,
-                                                      n_units, tables, preemph, dc, raw_out);
+                                                      n_units, tables, preemph, dc, raw_out, wave_item);
   return hipGetLastError();
+}
+
+void logmel_wave_items(const Item* items, int n_items, int unit0, int n_units, LogmelGrid g, int32_t* out) {
+  for (int b = 0; b < g.blocks; ++b) {
+    int wb, we;
+    logmel_share(g.blocks, b, g.waves, unit0, n_units, &wb, &we);
+    for (int w = 0; w < g.waves; ++w) {
+      const int u = wb + w;
+      int li = 0;
+      if (u < we) {
+        int hi = n_items - 1;
+        while (li < hi) {  // the last item whose unit_off <= u
+          const int mid = (li + hi + 1) >> 1;
+          if (items[mid].unit_off <= u) li = mid;
+          else hi = mid - 1;
+        }
+      }
+      out[(size_t)b * g.waves + w] = li;
+    }
+  }
 }
 
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
                          int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
-                         hipStream_t stream) {
+                         const int32_t* wave_item, hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
   Decode dc{pcm_scale, 1.0f / pcm_scale, 1.0 / (double)pcm_scale};  // the host's divisions are correctly rounded
-  // A launch with at least 4 units per wave on every CU's 12 waves takes one
-  // 12-wave workgroup per CU; smaller ones 4-wave workgroups, up to 3 per CU,
-  // each wave taking at least one unit (one per wave when they do not fill
-  // the machine, which spreads a small launch over more CUs).
-  if ((int64_t)n_units >= (int64_t)4 * kWavesBig * cus) {
-    const int want = (n_units + kWavesBig - 1) / kWavesBig;
+  const LogmelGrid g = logmel_grid(n_units, cus);
+  if (g.waves == kWavesBig)
     return launch_logmel_t<kWavesBig>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out,
-                                      want < cus ? want : cus, stream);
-  }
-  const int want = (n_units + kWavesSmall - 1) / kWavesSmall;
-  const int cap = kLogmelWavesPerSimd * cus;
+                                      g.blocks, wave_item, stream);
   return launch_logmel_t<kWavesSmall>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out,
-                                      want < cap ? want : cap, stream);
+                                      g.blocks, wave_item, stream);
 }
 
 template <typename O>

@@ -9,8 +9,8 @@ kernels writing s_memrealtime stamps (a 100 MHz clock common to all CUs,
 10 ns resolution; see sfe_debug_stamps in include/scriptrs_fe.h), and prints
 one JSON object:
   logmel: kernel span (first wave start to last wave end), spread of the
-    wave starts, prologue (wave start to its first unit), wave end
-    percentiles, units per wave and microseconds per unit;
+    wave starts, prologue (wave start to its first unit) and its steps,
+    wave end percentiles, units per wave and microseconds per unit;
   norm: span, and per workgroup the time to its first reduced statistics
     (loads landed), the statistics, and the stores, plus how many
     workgroups were in each phase at the median instant.
@@ -31,7 +31,7 @@ from . import _lib
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 TS_LIB = os.path.join(_HERE, "libscriptrs_fe_ts.so")
-LOGMEL_WORDS = 4 * 65536   # words before the normalisation region
+LOGMEL_WORDS = 8 * 65536   # words before the normalisation region (8 per wave)
 NORM_WORDS = 4 * 65536
 
 
@@ -59,20 +59,23 @@ def pct(a, q):
 
 def summarize(st: np.ndarray) -> dict:
     us = 0.01  # 10 ns ticks -> microseconds
-    lm = st[:LOGMEL_WORDS].reshape(-1, 4)
+    lm = st[:LOGMEL_WORDS].reshape(-1, 8)
     lm = lm[lm[:, 0] > 0]
     nm = st[LOGMEL_WORDS:].reshape(-1, 4)
     nm = nm[nm[:, 0] > 0]
     out = {}
     if len(lm):
         t0 = lm[:, 0].min()
-        start, first, end, units = ((lm[:, i] - (t0 if i < 3 else 0)).astype(np.float64) for i in range(4))
+        start, first, end, units, mel, itm = (
+            (lm[:, i] - (0 if i == 3 else t0)).astype(np.float64) for i in range(6))
         busy = units > 0
         per_unit = (end[busy] - first[busy]) / units[busy] * us
         out["logmel"] = {
             "waves": int(len(lm)), "span_us": float(end.max() * us),
             "start_spread_us": float(start.max() * us),
             "prologue_us": {"p50": pct((first - start) * us, 50), "p90": pct((first - start) * us, 90)},
+            # from the wave's start to its item descriptors' first use (p50)
+            "items_loaded_us_p50": pct((itm[busy] - start[busy]) * us, 50),
             "wave_end_us": {"p10": pct(end * us, 10), "p50": pct(end * us, 50), "p90": pct(end * us, 90),
                             "max": float(end.max() * us)},
             "units_per_wave": {"min": int(units.min()), "p50": pct(units, 50), "max": int(units.max())},

@@ -247,6 +247,14 @@ def test_build_rejects_mfma_destination_overlapping_its_operands():
     assert len(bad) == 2 and "v49" in bad[0] and "v51" in bad[1]
 
 
+def test_build_reads_spill_counts_from_kernel_metadata():
+    from scriptrs_amd.build import vgpr_spills
+    meta = ("    .name:           _ZN3sfe4kernAEv\n    .sgpr_count:     66\n    .vgpr_count:     168\n"
+            "    .vgpr_spill_count: 7\n  - .args:\n    .name:           _ZN3sfe4kernBEv\n"
+            "    .vgpr_count:     88\n    .vgpr_spill_count: 0\n")
+    assert vgpr_spills(meta) == {"_ZN3sfe4kernAEv": 7, "_ZN3sfe4kernBEv": 0}
+
+
 def test_build_counts_lane_masked_loops_per_kernel():
     from scriptrs_amd.build import lane_masked_loops
     asm = ("_ZN3sfe4kernAEv:\n\ts_andn2_b64 exec, exec, s[4:5]\n\ts_cbranch_execnz .LBB0_1\n"
