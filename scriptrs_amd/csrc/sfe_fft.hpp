@@ -6,7 +6,9 @@
 // The 256-point complex FFT is 16 x 16: each of 16 lanes runs a 16-point
 // DFT over its registers, the inter-stage twiddles are applied, the 16 x 16
 // block is transposed (through LDS in the kernel) and a second 16-point DFT
-// finishes it.  A 16-point DFT is an inner radix-4 layer, the internal
+// finishes it (the inter-stage twiddles in tangent form, their cosines
+// fused into the second DFT's inner layer).  A 16-point DFT is an inner
+// radix-4 layer, the internal
 // twiddles e^{-2 pi i p c / 16} and an outer radix-4 layer.  Its instruction
 // count is what the kernel's time goes to, so the constant multiplications
 // are folded into fused multiply-adds:
@@ -107,6 +109,35 @@ __host__ __device__ __forceinline__ void dft16_outer(cf (&a)[16]) {
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) a[i] = y[i];
+}
+
+// Inter-stage twiddle in tangent form: a e^{-i theta} = cos(theta) g with
+// g = (x + y tan(theta), y - x tan(theta)), two fmas; the cosine is applied
+// by the next stage (dft16_scaled).  Where cos(theta) is 0 the table holds
+// cos = 2^-100, tan = 2^100 (products exact in range: |x| < 2^27).
+__host__ __device__ __forceinline__ cf tan_twiddle(cf a, float t) {
+  return {fmaf(a.y, t, a.x), fmaf(-a.x, t, a.y)};
+}
+
+// 16-point forward DFT of the inputs c[m] a[m] (real scale factors, c[0] =
+// 1 and not read), into a[k], natural order.  The scales are fused into the
+// inner layer: per inner DFT (inputs p, p + 4, p + 8, p + 12) the first
+// input of each pair is scaled by a multiplication and the second by the
+// fmas of the pair's sum and difference.
+__host__ __device__ __forceinline__ void dft16_scaled(cf (&a)[16], const float (&c)[16]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const cf x0 = p == 0 ? a[0] : cf{c[p] * a[p].x, c[p] * a[p].y};
+    const cf x1 = {c[p + 4] * a[p + 4].x, c[p + 4] * a[p + 4].y};
+    const float c2 = c[p + 8], c3 = c[p + 12];
+    const cf t0 = cfma(c2, a[p + 8], x0), t1 = cfma(-c2, a[p + 8], x0);
+    const cf t2 = cfma(c3, a[p + 12], x1), t3 = cfma(-c3, a[p + 12], x1);
+    a[p] = cadd(t0, t2);
+    a[p + 8] = csub(t0, t2);
+    a[p + 4] = {t1.x + t3.y, t1.y - t3.x};   // t1 - i t3
+    a[p + 12] = {t1.x - t3.y, t1.y + t3.x};  // t1 + i t3
+  }
+  dft16_outer(a);
 }
 
 // 16-point forward DFT in registers: a[m] -> a[k], natural order.

@@ -147,7 +147,12 @@ static_assert(kMaxShareFrames * kRawTile / kTile * 4 + (int64_t)kMaxShareMembers
 // Constant tables, uploaded once per context.
 struct DevTables {
   float window[kNfft];       // hann_window(400), zero past 400
-  float2 tw256[256];         // [l * 16 + k1] = e^{-2 pi i l k1 / 256}, l, k1 < 16
+  // Inter-stage twiddles e^{-2 pi i l k1 / 256} (l, k1 < 16) in tangent
+  // form (sfe_fft.hpp tan_twiddle): tan256[l * 16 + k1] = tan, read by lane
+  // l of the first stage; cos256[k1 * 16 + l] = cos, read by lane k1 of the
+  // second stage (dft16_scaled).  At cos = 0 (l k1 = 64): 2^-100 and 2^100.
+  float tan256[256];
+  float cos256[256];
   // Split twiddles e^{-2 pi i k / 512}, k < 128, as (s, r): k < 64: (cos,
   // tan); k >= 64: (sin, cos / sin) (sfe_fft.hpp split_g).
   float2 split[128];

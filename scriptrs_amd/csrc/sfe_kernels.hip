@@ -212,14 +212,15 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     int n = 2 * l + 32 * m2;  // < 512, taps past 400 are zero
     wv[m2] = {tb->window[n], tb->window[n + 1]};
   }
-  cf t256[16];
+  // Inter-stage twiddles: tangents for this lane as a first-stage lane,
+  // cosines for it as a second-stage lane.  Per-lane table rows, indexed
+  // affinely: hipcc 7.2 (LLVM 22) miscompiled an equivalent
+  // tw[(l * k1) & 255] gather, loading .y of k1 = 1 from element 2l.
+  float tt[16], ct[16];
 #pragma unroll
   for (int k1 = 0; k1 < 16; ++k1) {
-    // A per-lane table row, indexed affinely: hipcc 7.2 (LLVM 22) miscompiled
-    // the equivalent tw[(l * k1) & 255] gather, loading .y of k1 = 1 from
-    // element 2l.
-    float2 tw = tb->tw256[l * 16 + k1];
-    t256[k1] = {tw.x, tw.y};
+    tt[k1] = tb->tan256[l * 16 + k1];
+    ct[k1] = tb->cos256[l * 16 + k1];
   }
   // split twiddles of bins l + 16 k2, k2 < 8, as (scale, tan or cot)
   float2 spt[8];
@@ -387,7 +388,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     cf a[16];
     dft16_windowed(zv, wv, a);  // window taps past 400 are zero
 #pragma unroll
-    for (int k1 = 1; k1 < 16; ++k1) a[k1] = cmul(a[k1], t256[k1]);
+    for (int k1 = 1; k1 < 16; ++k1) a[k1] = tan_twiddle(a[k1], tt[k1]);
 #pragma unroll
     for (int k1 = 0; k1 < 16; ++k1) X[k1 * kXStride + l] = a[k1];
     wave_lds_sync();
@@ -399,7 +400,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int m1 = 0; m1 < 16; ++m1) a[m1] = X[l * kXStride + m1];
-    dft16(a);  // a[k2] = Z[l + 16 k2]
+    dft16_scaled(a, ct);  // a[k2] = Z[l + 16 k2] (the twiddles' cosines applied here)
 
     // Split partner Z[256 - k] for k = l + 16 k2 lives in lane 16 - l,
     // register 15 - k2 (lane 0 pairs with itself, register (16 - k2) & 15).

@@ -65,11 +65,25 @@ void mel_filterbank(int n_fft, int n_mels, int sample_rate, float* out) {
 bool build_dev_tables(int sample_rate, DevTables* t) {
   memset(t, 0, sizeof(*t));
   hann_window(kWin, t->window);
-  for (int j = 0; j < 256; ++j) {
-    // laid out per lane so the kernel indexes it affinely (l * 16 + k1)
-    double a = -2.0 * M_PI * (double)((j / 16) * (j % 16)) / 256.0;
-    t->tw256[j] = make_float2((float)cos(a), (float)sin(a));
-  }
+  for (int l = 0; l < 16; ++l)
+    for (int k1 = 0; k1 < 16; ++k1) {
+      // e^{-i theta} = cos(theta) (1 - i tan(theta)), theta = 2 pi l k1 / 256;
+      // laid out per lane so the kernel indexes it affinely
+      const int m = (l * k1) % 256;
+      double c, tn;
+      if (m == 64 || m == 192) {
+        // cos = 0: a tiny cosine and a huge tangent with an exact product
+        // (sin = +-1 there)
+        c = ldexp(1.0, -100);
+        tn = (m == 64 ? 1.0 : -1.0) * ldexp(1.0, 100);
+      } else {
+        const double th = 2.0 * M_PI * (double)m / 256.0;
+        c = cos(th);
+        tn = sin(th) / c;
+      }
+      t->tan256[l * 16 + k1] = (float)tn;
+      t->cos256[k1 * 16 + l] = (float)c;
+    }
   for (int k = 0; k < 128; ++k) {
     const double b = 2.0 * M_PI * (double)k / 512.0, c = cos(b), s = sin(b);
     t->split[k] = k < 64 ? make_float2((float)c, (float)(s / c)) : make_float2((float)s, (float)(c / s));

@@ -1,9 +1,10 @@
 // Host run of the log-mel kernel's FFT arithmetic (scriptrs_amd/csrc/sfe_fft.hpp)
 // against float64 DFTs: the 16-point DFTs on their own, then the whole
 // 512-point real power spectrum of a frame as the kernel computes it (16
-// lanes x 16 registers, inter-stage twiddles from the device table, the
-// transpose, the second DFT, the even/odd split with the table's split
-// twiddles, bin 128 from Z[128]).  No GPU is used.
+// lanes x 16 registers, inter-stage twiddles from the device tables in
+// tangent form, the transpose, the second DFT applying their cosines, the
+// even/odd split with the table's split twiddles, bin 128 from Z[128]).
+// No GPU is used.
 //
 // Prints one line per check and "bad N" at the end (N checks failed).
 #include <math.h>
@@ -72,8 +73,40 @@ int main() {
     std::vector<C> yw = dft(xw);
     for (int k = 0; k < 16; ++k) e16w = fmax(e16w, std::abs(C(b[k].x, b[k].y) - yw[k]) / sqrt(nw) / u);
   }
+  // Twiddled inputs in tangent form, the cosines applied by dft16_scaled:
+  // the DFT of a[m] e^{-i theta_m}, including theta = pi/2 and 3 pi/2 (the
+  // tables' 2^-100 / 2^100 pair).
+  double e16s = 0;
+  std::uniform_real_distribution<double> ud(0.0, 2.0 * M_PI);
+  for (int trial = 0; trial < 2000; ++trial) {
+    cf a[16];
+    float c[16];
+    std::vector<C> x(16);
+    double nrm = 0;
+    for (int m = 0; m < 16; ++m) {
+      const cf v = {nd(rng), nd(rng)};
+      double th = m == 0 ? 0.0 : ud(rng);
+      if (trial % 7 == 0 && m == 5) th = M_PI / 2;
+      if (trial % 7 == 1 && m == 9) th = 3 * M_PI / 2;
+      double cc = cos(th), tn;
+      if (fabs(th - M_PI / 2) < 1e-12 || fabs(th - 3 * M_PI / 2) < 1e-12) {
+        cc = ldexp(1.0, -100);
+        tn = (th < M_PI ? 1.0 : -1.0) * ldexp(1.0, 100);
+      } else {
+        tn = sin(th) / cc;
+      }
+      a[m] = m == 0 ? v : sfe::tan_twiddle(v, (float)tn);
+      c[m] = m == 0 ? 1.0f : (float)cc;
+      x[m] = C(v.x, v.y) * std::polar(1.0, -th);
+      nrm += std::norm(x[m]);
+    }
+    sfe::dft16_scaled(a, c);
+    std::vector<C> y = dft(x);
+    for (int k = 0; k < 16; ++k) e16s = fmax(e16s, std::abs(C(a[k].x, a[k].y) - y[k]) / sqrt(nrm) / u);
+  }
   // A radix-4 x 4 DFT in f32: a few ulps of the input norm per output.
   check("dft16, max |err| / (|x| u)", e16, 16.0);
+  check("tan_twiddle + dft16_scaled, max |err| / (|x| u)", e16s, 24.0);
   check("dft16_windowed, max |err| / (|x w| u)", e16w, 16.0);
 
   // Whole frames: 4|X_k|^2 of the windowed 512-point frame
@@ -99,14 +132,18 @@ int main() {
         w[m2] = {tb.window[n], tb.window[n + 1]};
       }
       sfe::dft16_windowed(v, w, a);
-      for (int k1 = 1; k1 < 16; ++k1) a[k1] = sfe::cmul(a[k1], cf{tb.tw256[l * 16 + k1].x, tb.tw256[l * 16 + k1].y});
+      for (int k1 = 1; k1 < 16; ++k1) a[k1] = sfe::tan_twiddle(a[k1], tb.tan256[l * 16 + k1]);
       for (int k1 = 0; k1 < 16; ++k1) X[k1][l] = a[k1];
     }
     cf Z[256];
     for (int l = 0; l < 16; ++l) {
       cf a[16];
-      for (int m1 = 0; m1 < 16; ++m1) a[m1] = X[l][m1];
-      sfe::dft16(a);
+      float c[16];
+      for (int m1 = 0; m1 < 16; ++m1) {
+        a[m1] = X[l][m1];
+        c[m1] = tb.cos256[l * 16 + m1];
+      }
+      sfe::dft16_scaled(a, c);
       for (int k2 = 0; k2 < 16; ++k2) Z[l + 16 * k2] = a[k2];
     }
     float P[257];
