@@ -681,6 +681,39 @@ def test_norm_class_does_not_change_results(extractor):
             assert torch.equal(got, base), extra
 
 
+@pytest.mark.parametrize("frames", [(700, 1024), (1100, 1536)])
+def test_batch_split_into_calls_is_bitwise_the_same(extractor, frames):
+    """240 clips in one call (1,920 16-feature slabs of normalisation, more
+    than the GPU holds workgroups at once) and the same clips in four calls
+    of 60 give bitwise the same features: each call's longest clip is in the
+    same register class (16 or 24 rounds of 64 frames), and the sums run in
+    the same groups whatever the batch.  Clips of the full batch are also
+    checked against the oracle."""
+    import torch
+    lo, hi = frames
+    rng = np.random.default_rng(hi)
+    n, part = 240, 60  # 1920 slabs in one call: more than 4 workgroups on each of 256 CUs
+    T = rng.integers(lo, hi + 1, n)
+    T[::part] = hi
+    lens = (T - 1) * 160 + rng.integers(0, 160, n)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    flat = synth.speech_like(int(off[-1]), 31)
+    dev = torch.from_numpy(flat).cuda()
+    _flush(f"case: batch split into calls, {n} clips of {lo}-{hi} frames")
+    whole, fo = extractor.extract_batch(dev, off)
+    torch.cuda.synchronize()
+    whole = whole.cpu()
+    for p0 in range(0, n, part):
+        o = off[p0:p0 + part + 1]
+        got, _ = extractor.extract_batch(dev[int(o[0]):], o - o[0])
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), whole[128 * int(fo[p0]):128 * int(fo[p0 + part])]), p0
+    for i in (0, 1, n // 2, n - 1):
+        x = flat[off[i]:off[i + 1]]
+        got = whole[128 * int(fo[i]):128 * int(fo[i + 1])].numpy().reshape(128, -1)
+        assert_parity(got, oracle.extract(x), R.extract(x), R.f32_noise_envelope(x), what=f"clip {i}")
+
+
 def test_random_tables_shared_equal_own_bitwise(extractor):
     """150 random task tables over one 500 s recording (hop-aligned,
     arbitrary, clustered and duplicated starts; lengths 1 sample to 15 s):
