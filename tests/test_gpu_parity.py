@@ -468,6 +468,57 @@ def test_config3_full(extractor):
         assert_parity(got, want[sl].reshape(128, -1), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
 
 
+def test_long_form_past_2gib(extractor):
+    """A 12 h recording in one resident call: 2.6 GB of features and 2.3 GB
+    of raw log-mel, so chunks past the first 2 GiB of either are addressed
+    with 64-bit offsets.  Frame offsets exact, every chunk's rows normalised,
+    24 chunks at the start, middle and end bitwise equal to a separate call
+    of just those tasks, and chunks past 2 GiB of output against the oracle.  (The hour is
+    repeated with a different gain each time: synthesising 12 h takes
+    minutes.)"""
+    import torch
+    from scriptrs_amd import TaskTable, build_fast_execution_plan
+    _flush("case: 12 h resident, past 2 GiB")
+    hour = synth.speech_like(57_600_000, 3)
+    rec = np.concatenate([hour * np.float32(1.0 + 0.05 * k) for k in range(12)])
+    del hour
+    plan = build_fast_execution_plan(rec.size)
+    tasks = TaskTable(plan)
+    dev = torch.from_numpy(rec).cuda()
+    out, fo = extractor.extract_chunks(dev, tasks)
+    torch.cuda.synchronize()
+    assert np.array_equal(fo, tasks.frame_offsets)
+    assert 128 * 4 * int(fo[-1]) > 2**31 + 2**28
+    out = out.cpu().numpy()
+
+    def same_as_alone(first, count):
+        t2 = TaskTable(plan[first:first + count])
+        o2, _ = extractor.extract_chunks(dev, t2)
+        torch.cuda.synchronize()
+        o2 = o2.cpu().numpy()
+        seg = out[128 * int(fo[first]):128 * int(fo[first + count])]
+        bad = np.flatnonzero(seg.view(np.int32) != o2.view(np.int32))
+        if bad.size:
+            k = int(np.searchsorted(fo[first:first + count + 1] - fo[first], bad[0] // 128, side="right")) - 1
+            print(f"tasks {first}+{count}: {bad.size} differ, first at element {int(bad[0])} (task {first + k}),"
+                  f" max |diff| {float(np.abs(seg[bad] - o2[bad]).max()):.3g}", flush=True)
+        return bad.size == 0
+
+    # (24 tasks: calls of at most 16 items normalise with 8-wave workgroups,
+    # whose sums group the frames differently)
+    ok = [same_as_alone(0, 24), same_as_alone(tasks.n // 2, 24), same_as_alone(tasks.n - 24, 24)]
+    assert all(ok), ok
+    for i in range(tasks.n):
+        rows = out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1)
+        assert np.abs(rows.mean(axis=1)).max() < 1e-4, i
+    past = [i for i in range(tasks.n) if 128 * 4 * int(fo[i]) >= 2**31]
+    for i in (past[0], past[len(past) // 2], tasks.n - 1):
+        s0, s1 = (int(v) for v in tasks.array[i, :2])
+        a = rec[s0:s1]
+        got = out[128 * int(fo[i]):128 * int(fo[i + 1])].reshape(128, -1)
+        assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
+
+
 @pytest.mark.parametrize("seed", [101, 202, 303])
 def test_random_ragged_batch(extractor, seed):
     """48 clips of random lengths from 1 sample to 25 s (a few tiny ones
