@@ -197,6 +197,9 @@ int sfe_extract_chunks_padded(sfe_ctx* ctx, const float* recording, int64_t len,
  * ends) instead of the context's growable buffers, and calls no hipMalloc,
  * hipFree or other allocating routine (sfe_create reserves the host
  * buffers its planner uses, about 1.3 MB of pinned memory per context).
+ * Its first call on a device looks the array up (hipGetSymbolAddress;
+ * about 25 ms once per process while the code object holding the array
+ * loads).
  * Limits: at most 4096 tasks, and at most 64 MiB of raw log-mel, which is
  * 8192 tiles of 16 frames per task rounded up (131,072 frames, about 22
  * minutes of audio in 15 s chunks); larger calls return SFE_INVALID_ARG.

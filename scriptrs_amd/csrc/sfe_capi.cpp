@@ -177,7 +177,9 @@ struct sfe_ctx {
   int cus = 256;  // compute units of the device
   std::mutex mu;
   sfe::DevTables* d_tables = nullptr;
-  hipStream_t s_compute = nullptr;  // internal streams, default priority
+  // Internal streams (default priority) of the host-buffer entry points,
+  // created on first use (internal_streams).
+  hipStream_t s_compute = nullptr;
   hipStream_t s_copy = nullptr;
   DevBuf meta;      // Item tables
   std::vector<Item> meta_items;  // host copy of what meta holds (empty: unknown)
@@ -214,8 +216,8 @@ struct sfe_ctx {
   std::vector<hipEvent_t> tev;  // pairs: start, end; kind alternates logmel, norm
   size_t tev_used = 0;
   // This device's static scratch (sfe_extract_chunks_noalloc): item table,
-  // then raw log-mel.  Looked up at creation; h_meta is reserved for its
-  // largest item table at creation too.
+  // then raw log-mel.  Looked up by the entry point's first call on the
+  // context; h_meta is reserved for its largest item table at creation.
   unsigned char* noalloc = nullptr;
   // Host staging of its planner, also reserved at creation for
   // kNoAllocMaxItems items: the chunks' own items and the planner's lists.
@@ -450,6 +452,22 @@ int pcm_source(const void* p, int32_t pcm, int32_t bits, Source* out) {
   return SFE_OK;
 }
 
+// Creates the context's internal streams on their first use (each takes
+// milliseconds to create: most of what sfe_create took when it made them).
+// The caller holds ctx->mu.
+hipError_t internal_streams(sfe_ctx* ctx) {
+  hipError_t e = hipSuccess;
+  if (!ctx->s_compute && (e = hipStreamCreateWithFlags(&ctx->s_compute, hipStreamNonBlocking)) != hipSuccess) {
+    ctx->s_compute = nullptr;
+    return e;
+  }
+  if (!ctx->s_copy && (e = hipStreamCreateWithFlags(&ctx->s_copy, hipStreamNonBlocking)) != hipSuccess) {
+    ctx->s_copy = nullptr;
+    return e;
+  }
+  return hipSuccess;
+}
+
 int check_ctx(sfe_ctx* ctx) {
   if (!ctx) return fail(SFE_INVALID_ARG, "null context");
   hipError_t e = hipSetDevice(ctx->device);
@@ -571,15 +589,8 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
     if ((e = hipMalloc(&ctx->d_tables, sizeof(sfe::DevTables))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc"));
     if ((e = hipMemcpy(ctx->d_tables, &host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
       return cleanup(hip_fail(e, "hipMemcpy"));
-    if ((e = hipStreamCreateWithFlags(&ctx->s_compute, hipStreamNonBlocking)) != hipSuccess)
-      return cleanup(hip_fail(e, "hipStreamCreate"));
-    if ((e = hipStreamCreateWithFlags(&ctx->s_copy, hipStreamNonBlocking)) != hipSuccess)
-      return cleanup(hip_fail(e, "hipStreamCreate"));
     if ((e = hipEventCreateWithFlags(&ctx->ev_last, hipEventDisableTiming)) != hipSuccess)
       return cleanup(hip_fail(e, "hipEventCreate"));
-    void* na = nullptr;
-    if ((e = sfe::noalloc_scratch(device, &na)) != hipSuccess) return cleanup(hip_fail(e, "hipGetSymbolAddress(scratch)"));
-    ctx->noalloc = static_cast<unsigned char*>(na);
     if ((e = ctx->h_meta.reserve(sfe::kNoAllocItemBytes)) != hipSuccess) return cleanup(hip_fail(e, "hipHostMalloc"));
     ctx->na_in.reserve(sfe::kNoAllocMaxItems);
     ctx->na_ws.reserve(sfe::kNoAllocMaxItems);
@@ -634,6 +645,7 @@ int sfe_extract(sfe_ctx* ctx, const float* audio, int64_t len, float* out, int64
     SFE_HIP(ctx->io_out.reserve(out_bytes));
     SFE_HIP(ctx->h_io_in.reserve(in_bytes));
     SFE_HIP(ctx->h_io_out.reserve(out_bytes));
+    SFE_HIP(internal_streams(ctx));
     hipStream_t s = ctx->s_compute;
     parallel_memcpy(ctx->h_io_in.ptr, audio, in_bytes);
     SFE_HIP(hipMemcpyAsync(ctx->io_in.ptr, ctx->h_io_in.ptr, in_bytes, hipMemcpyHostToDevice, s));
@@ -802,9 +814,19 @@ int sfe_extract_chunks_noalloc(sfe_ctx* ctx, const float* recording, int64_t len
     SFE_HIP(sfe::noalloc_lock(ctx->device, &dev_lock));
     std::lock_guard<std::mutex> lock(ctx->mu);
     const size_t entries = (size_t)(sfe::kPlanEntriesPerItem + 1) * n;
-    if (!ctx->noalloc || ctx->h_meta.cap < entries * sizeof(Item) + sfe::kMaxLogmelWaves * sizeof(int32_t) ||
+    if (!ctx->noalloc) {
+      // The first call on this context looks up the device's static array
+      // (the first lookup in the process loads the code object that holds
+      // it, about 25 ms; kept out of sfe_create for callers that never use
+      // this entry point).  It allocates nothing: the array exists from the
+      // library's load.
+      void* na = nullptr;
+      SFE_HIP(sfe::noalloc_scratch(ctx->device, &na));
+      ctx->noalloc = static_cast<unsigned char*>(na);
+    }
+    if (ctx->h_meta.cap < entries * sizeof(Item) + sfe::kMaxLogmelWaves * sizeof(int32_t) ||
         ctx->na_in.capacity() < (size_t)n)
-      return fail(SFE_HIP_ERROR, "context has no static scratch");
+      return fail(SFE_HIP_ERROR, "context has no reserved planner buffers");
     int64_t fo = 0, own_tiles = 0;
     frame_offsets[0] = 0;
     ctx->na_in.clear();
@@ -994,6 +1016,7 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     SFE_HIP(ctx->win.reserve(2 * (size_t)half * es));
     if (!pinned)
       for (int b = 0; b < 2; ++b) SFE_HIP(ctx->h_win[b].reserve((size_t)half * es));
+    SFE_HIP(internal_streams(ctx));
     hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
     SFE_HIP(order_after_last(ctx, sc));
     SFE_HIP(order_after_last(ctx, sx));
