@@ -125,7 +125,10 @@ const char* sfe_last_error(void);
 /* ParakeetFeatureExtractor::new (src/frontend.rs:88-102).  Builds the
  * tables and uploads them to `device`.  The kernels are specialised to
  * n_fft 512, win 400, hop 160, 128 features; any other shape returns
- * SFE_INVALID_ARG.  sample_rate and preemphasis are free. */
+ * SFE_INVALID_ARG.  preemphasis is free; sample_rate sets the mel band
+ * edges, and every rate from 3.5 to 107 kHz fits one of the kernel's two
+ * mel schedules (outside it, a rate whose filters do not fit returns
+ * SFE_INVALID_ARG: sfe_debug_mel_schedule). */
 int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out);
 void sfe_destroy(sfe_ctx* ctx);
 
@@ -274,6 +277,13 @@ int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
  * this process, over all contexts.  It lets a test check that a call
  * allocated nothing. */
 int64_t sfe_debug_allocation_count(void);
+
+/* Test hook, no counterpart in the reference: the mel contraction schedule
+ * sfe_create would use for cfg (0: the default, which fits 16, 22.05 and
+ * 24 kHz; 1: the wider one, 50% more matrix steps), or -1 with SFE_INVALID_ARG's
+ * message in sfe_last_error when no schedule fits the filterbank (or the
+ * shape is unsupported).  No GPU is used. */
+int sfe_debug_mel_schedule(const sfe_config* cfg);
 
 /* Measurement hook, no counterpart in the reference.  In a library built
  * with -DSFE_TIMESTAMPS (python -m scriptrs_amd.build --timestamps, which

@@ -33,6 +33,13 @@ HOP = 160
 SAMPLE_RATE = 16000
 
 
+class _Config(ctypes.Structure):
+    """``sfo_config`` (sfe_oracle.c), the fields of ``TranscriptionConfig``
+    (src/config.rs:11-27) the front end reads."""
+    _fields_ = [("sample_rate", ctypes.c_int32), ("feature_size", ctypes.c_int32), ("n_fft", ctypes.c_int32),
+                ("win_length", ctypes.c_int32), ("hop_length", ctypes.c_int32), ("preemphasis", ctypes.c_float)]
+
+
 def build() -> str:
     """Compile the oracle with its Makefile (gcc); returns the .so path."""
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
@@ -58,6 +65,8 @@ def lib() -> ctypes.CDLL:
         L.sfo_extract_spans.restype = ctypes.c_int
         L.sfo_vad_frames.argtypes = [f32p, i64, f32p]
         L.sfo_vad_frames.restype = i64
+        L.sfo_extract_cfg.argtypes = [ctypes.POINTER(_Config), f32p, i64, f32p]
+        L.sfo_extract_cfg.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -113,6 +122,21 @@ def extract(audio: np.ndarray) -> np.ndarray:
     out = np.empty((N_MELS, num_frames(a.size)), np.float32)
     rc = lib().sfo_extract(_fp(a), a.size, _fp(out))
     if rc != 0:
+        raise ValueError("EmptyAudio")
+    return out
+
+
+def extract_cfg(audio: np.ndarray, sample_rate: int = SAMPLE_RATE, preemphasis: float = 0.97) -> np.ndarray:
+    """``extract`` under a ``TranscriptionConfig`` with another sample rate
+    (the mel filterbank's band edges, ``src/frontend.rs:188-223``) or
+    preemphasis coefficient (``src/frontend.rs:150-163``); the frame shape
+    stays n_fft 512, window 400, hop 160, 128 features."""
+    a = np.ascontiguousarray(audio, np.float32)
+    if a.size == 0:
+        raise ValueError("EmptyAudio")
+    c = _Config(sample_rate, N_MELS, N_FFT, WIN, HOP, preemphasis)
+    out = np.empty((N_MELS, num_frames(a.size)), np.float32)
+    if lib().sfo_extract_cfg(ctypes.byref(c), _fp(a), a.size, _fp(out)) != 0:
         raise ValueError("EmptyAudio")
     return out
 

@@ -24,7 +24,7 @@ EXPORTS = (
     "sfe_prepare_chunk", "sfe_extract_batch", "sfe_extract_chunks", "sfe_extract_chunks_pcm",
     "sfe_extract_chunks_padded", "sfe_extract_chunks_streamed", "sfe_extract_chunks_streamed_pcm",
     "sfe_set_frame_sharing", "sfe_set_timing", "sfe_get_timing", "sfe_vad_num_windows", "sfe_vad_frames", "sfe_extract_chunks_noalloc",
-    "sfe_debug_allocation_count", "sfe_debug_stamps",
+    "sfe_debug_allocation_count", "sfe_debug_mel_schedule", "sfe_debug_stamps",
 )
 
 
@@ -95,6 +95,7 @@ def lib() -> ctypes.CDLL:
         "sfe_set_timing": (ctypes.c_int, [vp, i32]),
         "sfe_get_timing": (ctypes.c_int, [vp, P(ctypes.c_double), P(ctypes.c_double), P(i32)]),
         "sfe_debug_allocation_count": (i64, []),
+        "sfe_debug_mel_schedule": (ctypes.c_int, [P(SfeConfig)]),
         "sfe_debug_stamps": (ctypes.c_int, [vp, i64]),
     }
     for name, (res, args) in sig.items():

@@ -77,9 +77,9 @@ def lane_masked_loops(asm: str, kernel: str) -> int:
 # round the loop together.  The compiler may instead structurise a loop with
 # lane-conditional code into a per-lane (exec-masked) loop in which lanes
 # leave at different iterations; a handoff probe built that way looped
-# forever.  The only per-lane loop these kernels may have is the copy of the
-# mel A operands into LDS (a strided per-thread loop, in the 4-wave form).
-LANE_LOOP_LIMITS = {"sfe_logmel_kernelI[fsi]Li12E": 0, "sfe_logmel_kernelI[fsi]Li4E": 1}
+# forever.  These kernels may have no per-lane loop at all.
+# (one entry per sample type t and mel schedule m of each workgroup size)
+LANE_LOOP_LIMITS = {"sfe_logmel_kernelI[t]Li12ELi[m]E": 0, "sfe_logmel_kernelI[t]Li4ELi[m]E": 0}
 
 
 def vgpr_spills(asm: str) -> dict[str, int]:
@@ -107,8 +107,8 @@ def check_asm(src: str, extra: list[str], verbose: bool = False) -> None:
     if spilled:
         raise RuntimeError(f"{src}: registers spilled in " + ", ".join(f"{k} ({n})" for k, n in spilled.items()))
     for pat, limit in LANE_LOOP_LIMITS.items():
-        for t in "fsi":
-            k = pat.replace("[fsi]", t)
+        for t, m in ((t, m) for t in "fsi" for m in "01"):
+            k = pat.replace("[t]", t).replace("[m]", m)
             n = lane_masked_loops(asm, k)
             if n > limit:
                 raise RuntimeError(f"{src}: {k} has {n} per-lane loops (at most {limit}): its work loop "

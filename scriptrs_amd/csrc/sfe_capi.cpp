@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <atomic>
 #include <exception>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
@@ -177,6 +178,7 @@ struct sfe_ctx {
   int cus = 256;  // compute units of the device
   std::mutex mu;
   sfe::DevTables* d_tables = nullptr;
+  int schedule = 0;  // the tables' mel schedule (sfe::DevTables::schedule)
   // Internal streams (default priority) of the host-buffer entry points,
   // created on first use (internal_streams).
   hipStream_t s_compute = nullptr;
@@ -317,7 +319,7 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* lm, const Item* d_l
       if (!(e[i] = timing_event(ctx))) return fail(SFE_HIP_ERROR, "hipEventCreate failed");
   if (e[0]) SFE_HIP(hipEventRecord(e[0], stream));
   if (stages & kLogmel)
-    SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_lm, n_lm, u0, u1 - u0, ctx->d_tables,
+    SFE_HIP(sfe::launch_logmel(src.ptr, src.pcm, src.scale, d_lm, n_lm, u0, u1 - u0, ctx->d_tables, ctx->schedule,
                                ctx->cfg.preemphasis, raw, ctx->cus, d_wave_item, stream));
   if (e[1]) SFE_HIP(hipEventRecord(e[1], stream));
   if (e[2]) SFE_HIP(hipEventRecord(e[2], stream));
@@ -578,6 +580,7 @@ int sfe_create(const sfe_config* cfg, int32_t device, sfe_ctx** out) {
     sfe_ctx* ctx = new sfe_ctx();
     ctx->cfg = *cfg;
     ctx->device = device;
+    ctx->schedule = host.schedule;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
       ctx->cus = cus;
@@ -1084,6 +1087,19 @@ int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable) {
 }
 
 int64_t sfe_debug_allocation_count(void) { return g_allocations.load(); }
+
+int sfe_debug_mel_schedule(const sfe_config* cfg) {
+  const int rc = guarded([&]() -> int {
+    if (!cfg) return fail(SFE_INVALID_ARG, "null argument");
+    std::string why;
+    if (!shape_supported(cfg, &why)) return fail(SFE_INVALID_ARG, why);
+    std::unique_ptr<sfe::DevTables> t(new sfe::DevTables);
+    if (!sfe::build_dev_tables(cfg->sample_rate, t.get()))
+      return fail(SFE_INVALID_ARG, "mel filter wider than the kernel's band table");
+    return -1 - t->schedule;  // (kept apart from the error codes)
+  });
+  return rc < 0 ? -1 - rc : -1;
+}
 
 int sfe_debug_stamps(void* device_buf, int64_t words) {
   if (!sfe::stamps_built()) return fail(SFE_INVALID_ARG, "this library was built without SFE_TIMESTAMPS");

@@ -22,16 +22,27 @@ constexpr int kPad = kNfft / 2;       // 256 zeros each side (src/frontend.rs:12
 // contracts the power spectra of its own 4 frames: an MFMA is 16 blocks of
 // [4 filters x 1 bin] . [1 bin x 4 frames].  Chain 0 holds the blocks of
 // filters 0..63 (block j: filters 4j..4j+3), chain 1 those of filters
-// 64..127.  Block j of chain c runs kChainSteps[c] consecutive bins from its
-// own first bin (a multiple of 4, from the device table), so the dense
-// 128x257 product is never formed.  The step counts fit the 16 kHz Slaney
-// filterbank (widest block of chain 0: 7 bins, of chain 1: 32).
+// 64..127.  Block j of chain c runs kChainSteps[schedule][c] consecutive
+// bins from its own first bin (a multiple of 4, from the device table), so
+// the dense 128x257 product is never formed.  Schedule 0 fits the Slaney
+// filterbank at 16, 22.05 and 24 kHz (at 16 kHz the widest block of chain 0
+// spans 7 bins, of chain 1 32); schedule 1, with 50% more steps, fits the
+// other sample rates from 3.5 to 107 kHz (at 8 kHz chain 0 needs 10 bins,
+// at 48 kHz chain 1 needs 41).  The tables take the first that fits.
 constexpr int kChains = 2;
-constexpr int kChainSteps[kChains] = {8, 32};
-constexpr int kMelSteps = 40;       // both chains
-constexpr int kMelVec = kMelSteps / 4;  // float4 A operands per lane
-static_assert(kChainSteps[0] + kChainSteps[1] == kMelSteps && kChainSteps[0] % 4 == 0 && kChainSteps[1] % 4 == 0,
-              "chains are whole float4 steps");
+constexpr int kSchedules = 2;
+constexpr int kChainSteps[kSchedules][kChains] = {{8, 32}, {12, 48}};
+constexpr int mel_vec(int schedule) { return (kChainSteps[schedule][0] + kChainSteps[schedule][1]) / 4; }
+// Power-spectrum bins each schedule's FFT stage writes per frame: the 257
+// bins, and for schedule 1 three zeros after them, so that a block whose
+// filters reach bin 256 can start at a multiple of 4 (the float4 operand
+// loads) and still run its 48 steps inside the written bins.
+constexpr int kBinsWritten[kSchedules] = {kBins, kBins + 3};
+constexpr int kMelVecMax = mel_vec(1);  // float4 A operands per lane, either schedule
+static_assert(kChainSteps[0][0] % 4 == 0 && kChainSteps[0][1] % 4 == 0 && kChainSteps[1][0] % 4 == 0 &&
+                  kChainSteps[1][1] % 4 == 0 && kChainSteps[0][0] <= kChainSteps[0][1] &&
+                  kChainSteps[1][0] <= kChainSteps[1][1] && mel_vec(0) <= kMelVecMax,
+              "chains are whole float4 steps, chain 1 the longer");
 
 // Raw log-mel (log2; times ln 2 is the log-mel) lives in scratch in tiles
 // of 16 frames (kRawTile floats): 8 slabs of 16 features, each [16 frames]
@@ -156,12 +167,14 @@ struct DevTables {
   // Split twiddles e^{-2 pi i k / 512}, k < 128, as (s, r): k < 64: (cos,
   // tan); k >= 64: (sin, cos / sin) (sfe_fft.hpp split_g).
   float2 split[128];
-  // A operands of the mel MFMAs: [v][lane] holds steps 4v..4v+3 (v < 2:
-  // chain 0, else chain 1, steps 4(v-2)..) of lane L = 4j + m: filter
-  // 64c + 4j + m at bin k0[c][j] + step, times 0.25 (the FFT stage yields
-  // 4|X|^2).
-  float4 mel_a[kMelVec][64];
+  // A operands of the mel MFMAs: [v][lane] holds steps 4v..4v+3 (v < S0 /
+  // 4: chain 0, else chain 1, steps 4(v - S0 / 4)..; S0 = chain 0's steps)
+  // of lane L = 4j + m: filter 64c + 4j + m at bin k0[c][j] + step, times
+  // 0.25 (the FFT stage yields 4|X|^2).  The first mel_vec(schedule) rows
+  // are used.
+  float4 mel_a[kMelVecMax][64];
   int32_t k0[kChains][16];  // first bin of each block (multiple of 4)
+  int32_t schedule;         // index into kChainSteps
 };
 
 // Host table builders (sfe_tables.cpp).
@@ -230,8 +243,9 @@ __host__ __device__ inline void logmel_share(int64_t G, int64_t b, int NW, int u
 constexpr int kMaxLogmelWaves = 4096;
 void logmel_wave_items(const Item* items, int n_items, int unit0, int n_units, LogmelGrid g, int32_t* out);
 // wave_item: the table above on the device for this launch, or null.
+// schedule: the tables' mel schedule (DevTables::schedule).
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
-                         int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
+                         int n_units, const DevTables* tables, int schedule, float preemph, float* raw_out, int cus,
                          const int32_t* wave_item, hipStream_t stream);
 // Normalises raw (f32 log2 values in 16-frame tiles, see Item) per (item, feature)
 // and writes feature-major [128][T] per item to out (f32, must not alias

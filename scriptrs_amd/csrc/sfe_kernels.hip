@@ -167,13 +167,15 @@ __device__ __forceinline__ void mfma_keep(const float4& a, const float4& b) {
   asm volatile("" ::"v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(b.x), "v"(b.y), "v"(b.z), "v"(b.w));
 }
 
-template <typename S, int NW>
+template <typename S, int NW, int SCH>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kLogmelWavesPerSimd, kLogmelWavesPerSimd)))
 void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ items, int n_items, int unit0,
                        int n_units, const DevTables* __restrict__ tb, float coef, Decode dc, float* __restrict__ out,
                        const int32_t* __restrict__ wave_item) {
   constexpr int kWaves = NW;
   constexpr int kThreads = 64 * NW;
+  constexpr int kS0 = kChainSteps[SCH][0], kS1 = kChainSteps[SCH][1];  // mel chain steps
+  constexpr int kMelVec = mel_vec(SCH);
   __shared__ __align__(16) float wbuf[kWaves][kWaveBuf];
   __shared__ __align__(16) float4 mel_a[kMelVec][64];
 
@@ -201,7 +203,9 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
   if (tid == 0) wg_next = wb + kWaves;  // each wave's first unit is wb + w
 
   // A operands of the mel MFMAs, shared by the workgroup's waves.
-  for (int i = tid; i < kMelVec * 64; i += kThreads) mel_a[i / 64][i % 64] = tb->mel_a[i / 64][i % 64];
+#pragma unroll
+  for (int i0 = 0; i0 < kMelVec * 64; i0 += kThreads)  // (a wave-uniform loop)
+    if (i0 + tid < kMelVec * 64) mel_a[(i0 + tid) / 64][(i0 + tid) % 64] = tb->mel_a[(i0 + tid) / 64][(i0 + tid) % 64];
   __syncthreads();
 
   // Per-lane constants: window taps of this lane's FFT inputs, inter-stage
@@ -429,6 +433,10 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
       P[256 - k] = pm;
     }
     if (l == 0) P[128] = 4.0f * fmaf(a[8].y, a[8].y, a[8].x * a[8].x);
+    if constexpr (kBinsWritten[SCH] > kBins) {
+      static_assert(kBinsWritten[SCH] - kBins <= 15 && kBinsWritten[SCH] <= kPStride, "zero bins fit the row");
+      if (l >= 1 && l <= kBinsWritten[SCH] - kBins) P[256 + l] = 0.0f;  // the zero bins after bin 256
+    }
     wave_lds_sync();
 
     // ---- 3. mel on the matrix cores: block j of chain c accumulates
@@ -441,31 +449,31 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     // instead of last: the accumulators start at it (chain 1's second
     // accumulator at zero).  Digital silence still sums to exactly 2^-24.
     f32x4 c0 = {kGuard, kGuard, kGuard, kGuard}, c1 = c0, c2 = {0.0f, 0.0f, 0.0f, 0.0f};
-    float4 a1n = mel_a[kChainSteps[0] / 4][lane], b1n = *reinterpret_cast<const float4*>(pb1);
+    float4 a1n = mel_a[kS0 / 4][lane], b1n = *reinterpret_cast<const float4*>(pb1);
     float4 a0n = mel_a[0][lane], b0n = *reinterpret_cast<const float4*>(pb0);
 #pragma unroll
-    for (int v = 0; v < kChainSteps[1] / 4; ++v) {
+    for (int v = 0; v < kS1 / 4; ++v) {
       const float4 a1 = a1n, b1 = b1n, a0 = a0n, b0 = b0n;
-      if (v + 1 < kChainSteps[1] / 4) {
-        a1n = mel_a[kChainSteps[0] / 4 + v + 1][lane];
+      if (v + 1 < kS1 / 4) {
+        a1n = mel_a[kS0 / 4 + v + 1][lane];
         b1n = *reinterpret_cast<const float4*>(pb1 + 4 * (v + 1));
       }
-      if (v + 1 < kChainSteps[0] / 4) {
+      if (v + 1 < kS0 / 4) {
         a0n = mel_a[v + 1][lane];
         b0n = *reinterpret_cast<const float4*>(pb0 + 4 * (v + 1));
       }
       c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.x, b1.x, c1, 0, 0, 0);
-      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.x, b0.x, c0, 0, 0, 0);
+      if (v < kS0 / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.x, b0.x, c0, 0, 0, 0);
       c2 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.y, b1.y, c2, 0, 0, 0);
-      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.y, b0.y, c0, 0, 0, 0);
+      if (v < kS0 / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.y, b0.y, c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.z, b1.z, c1, 0, 0, 0);
-      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.z, b0.z, c0, 0, 0, 0);
+      if (v < kS0 / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.z, b0.z, c0, 0, 0, 0);
       c2 = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.w, b1.w, c2, 0, 0, 0);
-      if (v < kChainSteps[0] / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.w, b0.w, c0, 0, 0, 0);
+      if (v < kS0 / 4) c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.w, b0.w, c0, 0, 0, 0);
       // The group's operands stay allocated past its MFMAs (see mfma_keep).
       __builtin_amdgcn_sched_barrier(0);
       mfma_keep(a1, b1);
-      if (v < kChainSteps[0] / 4) mfma_keep(a0, b0);
+      if (v < kS0 / 4) mfma_keep(a0, b0);
     }
     __builtin_amdgcn_s_setprio(0);
     acc0 = c0;
@@ -1055,21 +1063,32 @@ hipError_t set_stamp_buffer(void* buf, int64_t words) {
 int64_t tiles_for(int64_t T) { return (T + kTile - 1) / kTile; }
 int64_t units_for(int64_t T) { return (T + kQuad - 1) / kQuad; }
 
-template <int NW>
+template <int NW, int SCH>
 hipError_t launch_logmel_t(const void* samples, int pcm, const Decode& dc, const Item* items, int n_items, int unit0,
                            int n_units, const DevTables* tables, float preemph, float* raw_out, int grid,
                            const int32_t* wave_item, hipStream_t stream) {
   const dim3 g(grid), b(64 * NW);
   if (pcm == kPcmI16)
-    sfe_logmel_kernel<int16_t, NW><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items, unit0,
-                                                        n_units, tables, preemph, dc, raw_out, wave_item);
+    sfe_logmel_kernel<int16_t, NW, SCH><<<g, b, 0, stream>>>(static_cast<const int16_t*>(samples), items, n_items,
+                                                             unit0, n_units, tables, preemph, dc, raw_out, wave_item);
   else if (pcm == kPcmI32)
-    sfe_logmel_kernel<int32_t, NW><<<g, b, 0, stream>>>(static_cast<const int32_t*>(samples), items, n_items, unit0,
-                                                        n_units, tables, preemph, dc, raw_out, wave_item);
+    sfe_logmel_kernel<int32_t, NW, SCH><<<g, b, 0, stream>>>(static_cast<const int32_t*>(samples), items, n_items,
+                                                             unit0, n_units, tables, preemph, dc, raw_out, wave_item);
   else
-    sfe_logmel_kernel<float, NW><<<g, b, 0, stream>>>(static_cast<const float*>(samples), items, n_items, unit0,
-                                                      n_units, tables, preemph, dc, raw_out, wave_item);
+    sfe_logmel_kernel<float, NW, SCH><<<g, b, 0, stream>>>(static_cast<const float*>(samples), items, n_items, unit0,
+                                                           n_units, tables, preemph, dc, raw_out, wave_item);
   return hipGetLastError();
+}
+
+template <int NW>
+hipError_t launch_logmel_s(int schedule, const void* samples, int pcm, const Decode& dc, const Item* items,
+                           int n_items, int unit0, int n_units, const DevTables* tables, float preemph, float* raw_out,
+                           int grid, const int32_t* wave_item, hipStream_t stream) {
+  if (schedule == 1)
+    return launch_logmel_t<NW, 1>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out, grid,
+                                  wave_item, stream);
+  return launch_logmel_t<NW, 0>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out, grid,
+                                wave_item, stream);
 }
 
 void logmel_wave_items(const Item* items, int n_items, int unit0, int n_units, LogmelGrid g, int32_t* out) {
@@ -1093,16 +1112,16 @@ void logmel_wave_items(const Item* items, int n_items, int unit0, int n_units, L
 }
 
 hipError_t launch_logmel(const void* samples, int pcm, float pcm_scale, const Item* items, int n_items, int unit0,
-                         int n_units, const DevTables* tables, float preemph, float* raw_out, int cus,
+                         int n_units, const DevTables* tables, int schedule, float preemph, float* raw_out, int cus,
                          const int32_t* wave_item, hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
   Decode dc{pcm_scale, 1.0f / pcm_scale, 1.0 / (double)pcm_scale};  // the host's divisions are correctly rounded
   const LogmelGrid g = logmel_grid(n_units, cus);
   if (g.waves == kWavesBig)
-    return launch_logmel_t<kWavesBig>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out,
-                                      g.blocks, wave_item, stream);
-  return launch_logmel_t<kWavesSmall>(samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph, raw_out,
-                                      g.blocks, wave_item, stream);
+    return launch_logmel_s<kWavesBig>(schedule, samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph,
+                                      raw_out, g.blocks, wave_item, stream);
+  return launch_logmel_s<kWavesSmall>(schedule, samples, pcm, dc, items, n_items, unit0, n_units, tables, preemph,
+                                      raw_out, g.blocks, wave_item, stream);
 }
 
 template <typename O>

@@ -92,31 +92,43 @@ bool build_dev_tables(int sample_rate, DevTables* t) {
   mel_filterbank(kNfft, kMel, sample_rate, fb.data());
   // 4-filter blocks: the first bin (a multiple of 4) is chosen here; the
   // block's nonzero bins must fit its chain's step count, and every bin
-  // read must lie within the 257 bins the FFT stage writes.
-  for (int c = 0; c < kChains; ++c) {
-    const int S = kChainSteps[c];
-    for (int j = 0; j < 16; ++j) {
-      const int f0 = 64 * c + 4 * j;
-      int lo = -1, hi = -1;
-      for (int m = f0; m < f0 + 4; ++m)
-        for (int k = 0; k < kBins; ++k)
-          if (fb[(size_t)m * kBins + k] != 0.0f) {
-            if (lo < 0 || k < lo) lo = k;
-            if (k > hi) hi = k;
+  // read must lie within the bins the FFT stage writes (kBinsWritten).  The
+  // first schedule every block fits is used.
+  auto fill = [&](int sch) -> bool {
+    for (int c = 0; c < kChains; ++c) {
+      const int S = kChainSteps[sch][c];
+      for (int j = 0; j < 16; ++j) {
+        const int f0 = 64 * c + 4 * j;
+        int lo = -1, hi = -1;
+        for (int m = f0; m < f0 + 4; ++m)
+          for (int k = 0; k < kBins; ++k)
+            if (fb[(size_t)m * kBins + k] != 0.0f) {
+              if (lo < 0 || k < lo) lo = k;
+              if (k > hi) hi = k;
+            }
+        if (lo < 0) lo = hi = 0;
+        int k0 = lo / 4 * 4;
+        if (k0 + S > kBinsWritten[sch]) k0 = (kBinsWritten[sch] - S) / 4 * 4;
+        if (lo < k0 || hi >= k0 + S) return false;  // filters too wide for this schedule
+        t->k0[c][j] = k0;
+        for (int s = 0; s < S; ++s)
+          for (int m = 0; m < 4; ++m) {
+            const int v = (c == 0 ? 0 : kChainSteps[sch][0] / 4) + s / 4;
+            float* a = reinterpret_cast<float*>(&t->mel_a[v][4 * j + m]);
+            a[s % 4] = fb[(size_t)(f0 + m) * kBins + k0 + s] * 0.25f;
           }
-      if (lo < 0) lo = hi = 0;
-      int k0 = lo / 4 * 4;
-      if (k0 + S > kBins) k0 = (kBins - S) / 4 * 4;
-      if (lo < k0 || hi >= k0 + S) return false;  // filters too wide for this schedule
-      t->k0[c][j] = k0;
-      for (int s = 0; s < S; ++s)
-        for (int m = 0; m < 4; ++m) {
-          const int v = (c == 0 ? 0 : kChainSteps[0] / 4) + s / 4;
-          float* a = reinterpret_cast<float*>(&t->mel_a[v][4 * j + m]);
-          a[s % 4] = fb[(size_t)(f0 + m) * kBins + k0 + s] * 0.25f;
-        }
+      }
     }
+    t->schedule = sch;
+    return true;
+  };
+  bool ok = false;
+  for (int sch = 0; sch < kSchedules && !ok; ++sch) {
+    memset(t->mel_a, 0, sizeof(t->mel_a));
+    memset(t->k0, 0, sizeof(t->k0));
+    ok = fill(sch);
   }
+  if (!ok) return false;
   return true;
 }
 

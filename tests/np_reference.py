@@ -52,16 +52,18 @@ def slaney_mel_filterbank(n_fft: int = N_FFT, n_mels: int = N_MELS, sr: int = SR
     return w * (2.0 / (mel_f[2:n_mels + 2] - mel_f[:n_mels]))[:, None]
 
 
-def logmel_raw(audio: np.ndarray, window=None, fb=None) -> np.ndarray:
-    """ln(mel + 2^-24), [128, T] float64, before normalisation."""
+def logmel_raw(audio: np.ndarray, window=None, fb=None, sr: int = SR, preemph: float = 0.97) -> np.ndarray:
+    """ln(mel + 2^-24), [128, T] float64, before normalisation (sample rate
+    sr sets the filterbank's band edges; preemph the preemphasis
+    coefficient, an f32 value as in the reference's config)."""
     x = np.asarray(audio, np.float64)
     if x.size == 0:
         raise ValueError("EmptyAudio")
     w = (hann_window_f32() if window is None else window).astype(np.float64)
-    fb = slaney_mel_filterbank() if fb is None else np.asarray(fb, np.float64)
+    fb = slaney_mel_filterbank(sr=sr) if fb is None else np.asarray(fb, np.float64)
     y = np.empty_like(x)
     y[0] = x[0]
-    y[1:] = x[1:] - np.float64(np.float32(0.97)) * x[:-1]
+    y[1:] = x[1:] - np.float64(np.float32(preemph)) * x[:-1]
     padded = np.concatenate([np.zeros(N_FFT // 2), y, np.zeros(N_FFT // 2)])
     T = x.size // HOP + 1
     idx = np.arange(T)[:, None] * HOP + np.arange(WIN)[None, :]
@@ -79,9 +81,9 @@ def normalize(raw: np.ndarray) -> np.ndarray:
     return (raw - mean) / (np.sqrt(var) + 1e-5)
 
 
-def extract(audio: np.ndarray) -> np.ndarray:
+def extract(audio: np.ndarray, sr: int = SR, preemph: float = 0.97) -> np.ndarray:
     """Feature-major [128, T] float64 normalised log-mel."""
-    return normalize(logmel_raw(audio))
+    return normalize(logmel_raw(audio, sr=sr, preemph=preemph))
 
 
 # An element is near the noise floor when its float64 mel energy is at most
@@ -95,30 +97,30 @@ NEAR_GUARD_RATIO = 1e-6
 ENV_CAP = 5e-3
 
 
-def _frames_f64(audio: np.ndarray):
+def _frames_f64(audio: np.ndarray, preemph: float = 0.97):
     x = np.asarray(audio, np.float64)
     w = hann_window_f32().astype(np.float64)
     y = np.empty_like(x)
     y[0] = x[0]
-    y[1:] = x[1:] - np.float64(np.float32(0.97)) * x[:-1]
+    y[1:] = x[1:] - np.float64(np.float32(preemph)) * x[:-1]
     padded = np.concatenate([np.zeros(N_FFT // 2), y, np.zeros(N_FFT // 2)])
     T = x.size // HOP + 1
     idx = np.arange(T)[:, None] * HOP + np.arange(WIN)[None, :]
     return padded[idx] * w[None, :]
 
 
-def near_guard(audio: np.ndarray) -> np.ndarray:
+def near_guard(audio: np.ndarray, sr: int = SR, preemph: float = 0.97) -> np.ndarray:
     """[128, T] bool: elements whose float64 mel energy is at most
     NEAR_GUARD_RATIO of their frame's energy (frames of zero energy are
     exact in every implementation and are not near-guard)."""
-    frames = _frames_f64(audio)
+    frames = _frames_f64(audio, preemph)
     P = np.abs(np.fft.rfft(frames, n=N_FFT, axis=1)) ** 2
-    mel = P @ slaney_mel_filterbank().T
+    mel = P @ slaney_mel_filterbank(sr=sr).T
     E = P.sum(1, keepdims=True)
     return ((mel <= NEAR_GUARD_RATIO * E) & (E > 0)).T
 
 
-def f32_noise_envelope(audio: np.ndarray, parts: bool = False):
+def f32_noise_envelope(audio: np.ndarray, parts: bool = False, sr: int = SR, preemph: float = 0.97):
     """Per-element scale of the rounding noise any f32 FFT-based implementation
     of the front end carries, in normalised units, [128, T].
 
@@ -137,8 +139,8 @@ def f32_noise_envelope(audio: np.ndarray, parts: bool = False):
     std).  It is zero in rows without near-guard elements and at most
     ENV_CAP.  Only elements with a non-zero envelope may be widened past the
     flat bar.  Returns elem + row, or (elem, row) with parts."""
-    frames = _frames_f64(audio)
-    fb = slaney_mel_filterbank()
+    frames = _frames_f64(audio, preemph)
+    fb = slaney_mel_filterbank(sr=sr)
     T = frames.shape[0]
     X = np.abs(np.fft.rfft(frames, n=N_FFT, axis=1))
     u = 2.0 ** -24

@@ -74,6 +74,30 @@ def test_tables_bit_exact_with_oracle():
     assert np.array_equal(fb2, oracle.mel_filterbank(512, 128, 22050))
 
 
+def test_mel_schedule_by_sample_rate():
+    """The mel contraction schedule sfe_create takes for each sample rate:
+    the default one at 16, 22.05 and 24 kHz (and some rates near them); the
+    wider one (50% more matrix steps) at 8, 11.025, 32, 44.1, 48 and 96 kHz;
+    one or the other for every rate from 3.5 to 107 kHz tried here; none
+    (SFE_INVALID_ARG) where no schedule fits the Slaney filterbank, and for
+    another shape."""
+    import ctypes
+    from scriptrs_amd import _lib
+
+    def schedule(**kw):
+        c = TranscriptionConfig(**kw).to_c()
+        return _lib.lib().sfe_debug_mel_schedule(ctypes.byref(c))
+
+    assert [schedule(sample_rate=sr) for sr in (16000, 22050, 24000)] == [0, 0, 0]
+    assert [schedule(sample_rate=sr) for sr in (8000, 11025, 32000, 44100, 48000, 96000)] == [1] * 6
+    rates = list(range(3500, 8000, 500)) + list(range(8000, 107001, 1000)) + [11025, 44100, 88200]
+    assert all(schedule(sample_rate=sr) in (0, 1) for sr in rates)
+    for sr in (2500, 3000, 108000):
+        assert schedule(sample_rate=sr) == -1
+        assert "band table" in _lib.last_error()
+    assert schedule(n_fft=1024) == -1 and "unsupported frontend shape" in _lib.last_error()
+
+
 LENGTHS = [0, 1, 1279, 1280, 95_999, 96_000, 238_079, 238_080, 238_081, 240_000, 240_001, 444_160,
            444_161, 650_240, 1_000_003, 57_600_000, 460_800_000]
 

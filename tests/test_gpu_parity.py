@@ -519,6 +519,44 @@ def test_long_form_past_2gib(extractor):
         assert_parity(got, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"chunk {i}")
 
 
+@pytest.mark.parametrize("sr,pre", [(8000, 0.97), (11025, 0.97), (22050, 0.97), (44100, 0.97), (48000, 0.97),
+                                    (16000, 0.0), (16000, 0.5)])
+def test_other_sample_rates_and_preemphasis(sr, pre):
+    """A TranscriptionConfig with another sample rate (the mel filterbank's
+    band edges; at 8, 11.025, 44.1 and 48 kHz the filters need the wider mel
+    schedule, at 22.05 kHz the default one fits) or another preemphasis
+    coefficient (src/config.rs:11-27, src/frontend.rs:150-223), against the
+    oracle under the same config: one 10 s clip (extract, 4-wave launch) and
+    64 clips of 125,000 samples (extract_batch, the 12-wave launch).  Filters
+    that fall between FFT bins (the 11 and 13 lowest at 44.1 and 48 kHz)
+    give constant rows, bitwise equal to the oracle's replay of the
+    reference's sequential f32 sums."""
+    import torch
+    from scriptrs_amd import ParakeetFeatureExtractor, TranscriptionConfig
+    _flush(f"case: sample rate {sr}, preemphasis {pre}")
+    ext = ParakeetFeatureExtractor(TranscriptionConfig(sample_rate=sr, preemphasis=pre))
+    empty = ~oracle.mel_filterbank(512, 128, sr).any(axis=1)
+
+    def check(got, a, what):
+        want = oracle.extract_cfg(a, sr, pre)
+        assert np.array_equal(got[empty].view(np.int32), want[empty].view(np.int32)), what
+        assert_parity(got[~empty], want[~empty], R.extract(a, sr=sr, preemph=pre)[~empty],
+                      R.f32_noise_envelope(a, sr=sr, preemph=pre)[~empty], what=what)
+
+    try:
+        a = synth.speech_like(10 * sr, 9)
+        check(np.ascontiguousarray(ext.extract(a).T), a, f"{sr} Hz clip")
+        x = synth.speech_like(64 * 125_000, 10)
+        off = np.arange(65, dtype=np.int64) * 125_000
+        out, fo = ext.extract_batch(torch.from_numpy(x).cuda(), off)
+        torch.cuda.synchronize()
+        out = out.cpu().numpy()
+        for i in (0, 31, 63):
+            check(out[128 * fo[i]:128 * fo[i + 1]].reshape(128, -1), x[off[i]:off[i + 1]], f"{sr} Hz batch clip {i}")
+    finally:
+        ext.close()
+
+
 @pytest.mark.parametrize("seed", [101, 202, 303])
 def test_random_ragged_batch(extractor, seed):
     """48 clips of random lengths from 1 sample to 25 s (a few tiny ones
