@@ -304,6 +304,13 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
     for (int h = 0; h < kSpanVec; ++h) cv[h] = Pcm<S>::dec4(nv[h], dc);
     const float cxm1 = Pcm<S>::dec(nxm1, dc);
 
+    // From here to the FFT's input reads the wave runs at priority 1: the
+    // span's LDS writes, the previous quad's stores and the next quad's
+    // loads are a round trip the wave waits on before any arithmetic, and
+    // issuing it ahead of the SIMD's other waves (in their FFT arithmetic)
+    // shortens that wait (log-mel -1.6% on the 1 h workload, -3% on the
+    // 64-clip batch; priority 2 here was less good).
+    __builtin_amdgcn_s_setprio(1);
     // ---- 1. preemphasised, zero-padded samples of this wave's 4 frames
     // y[0] = x[0], y[s] = x[s] - coef * x[s-1] (separately rounded, as
     // src/frontend.rs:157 computes it), zero outside [0, L).  The previous
@@ -389,6 +396,7 @@ void sfe_logmel_kernel(const S* __restrict__ samples, const Item* __restrict__ i
       zv[12] = {v.x, v.y};
     }
     wave_lds_sync();  // the transpose below reuses the span's LDS
+    __builtin_amdgcn_s_setprio(0);
     cf a[16];
     dft16_windowed(zv, wv, a);  // window taps past 400 are zero
 #pragma unroll
