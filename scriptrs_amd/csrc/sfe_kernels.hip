@@ -759,7 +759,12 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
   __shared__ double red[W * F];
   __shared__ int redi[W * (F / 4)];
   __shared__ float st[3 * F];
-  __shared__ __align__(16) float tb[F * S::kTStride];
+  // Two transpose buffers in the 4-wave form (chunk ch stages into tb[ch %
+  // 2]: the next chunk's staging does not wait for this chunk's stores, one
+  // barrier per chunk); one in the 8-wave form, whose buffer is twice as
+  // large.
+  constexpr int kTBufs = W == 4 ? 2 : 1;
+  __shared__ __align__(16) float tb[kTBufs][F * S::kTStride];
   const int item = work / S::kSlabs;
   if (item >= n_items) return;
 #ifdef SFE_TIMESTAMPS
@@ -924,16 +929,17 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
 #pragma unroll
       for (int ch = 0; ch < (N + X) / 4; ++ch) {
         if (ch < chunks) {
+          float* t = tb[ch % kTBufs];
           if (ch < N / 4) {
 #pragma unroll
-            for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, v[4 * ch + jr]);
+            for (int jr = 0; jr < 4; ++jr) stage<W, F>(t, q, kSpan * jr + fr, v[4 * ch + jr]);
           } else {
 #pragma unroll
-            for (int jr = 0; jr < 4; ++jr) stage<W, F>(tb, q, kSpan * jr + fr, reload(4 * ch + jr));
+            for (int jr = 0; jr < 4; ++jr) stage<W, F>(t, q, kSpan * jr + fr, reload(4 * ch + jr));
           }
           __syncthreads();
-          store_chunk<W, F>(tb, st, kChunk * ch, T, rs, lane, w, ob);
-          __syncthreads();
+          store_chunk<W, F>(t, st, kChunk * ch, T, rs, lane, w, ob);
+          if (kTBufs == 1) __syncthreads();
         }
       }
 #ifdef SFE_TIMESTAMPS
@@ -1005,12 +1011,13 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
       const int j = 4 * ch + jr;
       e[jr] = ln2_scale(*(j < nr ? round(j) : p0));
     }
+    float* t = tb[ch % kTBufs];
 #pragma unroll
     for (int jr = 0; jr < 4; ++jr)
-      if (4 * ch + jr < nr) stage<W, F>(tb, q, kSpan * jr + fr, e[jr]);
+      if (4 * ch + jr < nr) stage<W, F>(t, q, kSpan * jr + fr, e[jr]);
     __syncthreads();
-    store_chunk<W, F>(tb, st, kChunk * ch, T, rs, lane, w, ob);
-    __syncthreads();
+    store_chunk<W, F>(t, st, kChunk * ch, T, rs, lane, w, ob);
+    if (kTBufs == 1) __syncthreads();
   }
 #ifdef SFE_TIMESTAMPS
   if (threadIdx.x == 0) SFE_STAMP(sn + 3, stamp_now());
