@@ -839,7 +839,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
         float a = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-          if (j < nr) a += comp(v[j], c) - comp(x0, c);
+          a += comp(v[j], c) - comp(x0, c);  // exactly 0 for the x0 padding past nr
           eq[c] = eq[c] && (comp(v[j], c) == comp(x0, c));
           if ((j + 1) % kNormFlush == 0 || j + 1 == N) {
             s[c] += (double)a;
@@ -869,7 +869,7 @@ __device__ __forceinline__ void norm_body(const float* __restrict__ raw, const I
           for (int c = 0; c < 4; ++c) {
 #pragma unroll
             for (int jr = 0; jr < 4; ++jr) {
-              if (N + 4 * g + jr < nr) a[c] += comp(e[jr], c) - comp(x0, c);
+              a[c] += comp(e[jr], c) - comp(x0, c);  // exactly 0 past nr (x0)
               eq[c] = eq[c] && (comp(e[jr], c) == comp(x0, c));
             }
             if ((4 * g + 4) % kNormFlush == 0) {
