@@ -109,6 +109,12 @@ struct DevBuf {
     cap = 0;
     e = hipMalloc(&ptr, want);
     g_allocations.fetch_add(1);
+    if (e != hipSuccess && want > bytes) {  // the headroom does not fit: exactly what is asked
+      (void)hipGetLastError();
+      want = bytes;
+      e = hipMalloc(&ptr, want);
+      g_allocations.fetch_add(1);
+    }
     if (e == hipSuccess) cap = want;
     return e;
   }
