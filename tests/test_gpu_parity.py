@@ -520,12 +520,13 @@ def test_long_form_past_2gib(extractor):
 
 
 @pytest.mark.parametrize("sr,pre", [(8000, 0.97), (11025, 0.97), (22050, 0.97), (44100, 0.97), (48000, 0.97),
-                                    (16000, 0.0), (16000, 0.5)])
+                                    (3500, 0.97), (96000, 0.97), (107000, 0.97), (16000, 0.0), (16000, 0.5)])
 def test_other_sample_rates_and_preemphasis(sr, pre):
     """A TranscriptionConfig with another sample rate (the mel filterbank's
     band edges; at 8, 11.025, 44.1 and 48 kHz the filters need the wider mel
     schedule, at 22.05 kHz the default one fits) or another preemphasis
-    coefficient (src/config.rs:11-27, src/frontend.rs:150-223), against the
+    coefficient (src/config.rs:11-27, src/frontend.rs:150-223; 3.5 and 107 kHz
+    are the ends of the range sfe_create takes), against the
     oracle under the same config: one 10 s clip (extract, 4-wave launch) and
     64 clips of 125,000 samples (extract_batch, the 12-wave launch).  Filters
     that fall between FFT bins (the 11 and 13 lowest at 44.1 and 48 kHz)

@@ -274,13 +274,14 @@ def test_oracle_misses_the_flat_bar_only_on_near_guard_elements(kind, seed):
           f"({int(near.sum())} near-guard elements)")
 
 
-@pytest.mark.parametrize("sr,pre", [(8000, 0.97), (22050, 0.97), (48000, 0.97), (16000, 0.0), (16000, 0.5)])
+@pytest.mark.parametrize("sr,pre", [(8000, 0.97), (22050, 0.97), (48000, 0.97), (3500, 0.97), (107000, 0.97),
+                                    (16000, 0.0), (16000, 0.5)])
 def test_oracle_other_configs_against_float64(sr, pre):
     """extract_cfg (another sample rate, another preemphasis) against the
     float64 numpy restatement under the same config: within the flat bar
     except where the envelope allows, as at the default config; and the
     config is really applied (the default differs by far more).
-    At 48 kHz the 13 lowest filters fall between FFT bins (their f32 rows are
+    At 48 kHz the 13 lowest filters (at 107 kHz the 27 lowest) fall between FFT bins (their f32 rows are
     all zero): those rows are digital silence, constant in every frame, and
     the oracle replays the reference's sequential f32 sums there (about
     -0.94 where float64 gives 0, as for silent audio); they are checked to
@@ -291,7 +292,7 @@ def test_oracle_other_configs_against_float64(sr, pre):
     o = oracle.extract_cfg(a, sr, pre)
     env = R.f32_noise_envelope(a, sr=sr, preemph=pre)
     empty = ~oracle.mel_filterbank(512, 128, sr).any(axis=1)
-    assert empty.sum() == (13 if sr == 48000 else 0)
+    assert empty.sum() == {48000: 13, 107000: 27}.get(sr, 0)
     assert np.all(o[empty] == o[empty][:, :1])
     excess = np.abs(o - r) - (1e-4 + 1e-3 * np.abs(r))
     assert np.all(excess[~empty] <= 8.0 * env[~empty])
