@@ -121,6 +121,24 @@ def test_planner_configs(cfg):
         assert [(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples) for t in got] == want
 
 
+def test_planner_random_configs_match_oracle():
+    """Property test over random planner configs (overlap seconds, context
+    and model-sample limits, including the saturating and degenerate ends)
+    and recording lengths: the library's task table equals the restated
+    planner's (src/long_form/planner.rs:94-137, src/long_form.rs:566-582)."""
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=300, deadline=None, derandomize=True)
+    @given(ov=st.floats(-10.0, 100.0, allow_nan=False), ctx=st.integers(0, 60_000),
+           mx=st.integers(0, 1_500_000), n=st.integers(0, 20_000_000))
+    def check(ov, ctx, mx, n):
+        got = OverlapChunkConfig(ov, ctx, mx).tasks(n)
+        want = _oracle_tasks(planner.OverlapChunkConfig(ov, ctx, mx), n)
+        assert [(t.audio_start, t.audio_end, t.global_sample_offset, t.context_samples) for t in got] == want
+
+    check()
+
+
 def _oracle_tasks(o, n):
     out = []
     for s, e in o.plan(0, n):
