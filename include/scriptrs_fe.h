@@ -33,7 +33,7 @@ extern "C" {
 #endif
 
 /* Status codes.  They map onto the reference's TranscriptionError
- * (src/error.rs:5-40) as the INTEGRATION notes describe:
+ * (src/error.rs:5-40) as follows:
  *   SFE_EMPTY_AUDIO     -> EmptyAudio                  (src/frontend.rs:105-107)
  *   SFE_AUDIO_TOO_LONG  -> AudioTooLong{..}            (src/pipeline.rs:153-158, :205-210)
  *   SFE_INVALID_ARG     -> InvalidModelOutput(message)
