@@ -240,7 +240,9 @@ int sfe_vad_frames(sfe_ctx* ctx, const void* recording, int32_t pcm_format, int3
  * task that ends inside it, plus its left halo.  Consecutive windows form
  * batches of about 64 MB (1 to 64 windows), each copied host->device as one
  * contiguous range and featurized by one launch, double-buffered on two
- * streams: the copy of batch b+1 overlaps the compute of batch b.  Device
+ * streams: the copy of batch b+1 overlaps the compute of batch b.  Frames
+ * that overlapping tasks of one batch share are computed once
+ * (sfe_set_frame_sharing), with the same output.  Device
  * memory for the copies: two batches.  `out` is a device buffer sized as for
  * sfe_extract_chunks.  A pinned (page-locked) `host` buffer is copied
  * directly; a pageable one is staged through pinned buffers.  Synchronous:
@@ -261,14 +263,15 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
 /* ---- tuning and instrumentation (no reference counterpart) ----------- */
 
 /* Shared frames: on by default.  Overlapping chunk tasks of one call
- * (sfe_extract_chunks, _pcm, _padded, sfe_extract_batch) whose starts agree
+ * (sfe_extract_chunks, _pcm, _padded, sfe_extract_batch; in the streamed
+ * entry points, the tasks of one batch of windows) whose starts agree
  * modulo the hop have identical log-mel for a frame whose 512 padded
  * samples lie, in every task that holds it, after the task's first sample
  * and before its end; such frames are computed once and each task keeps
  * its first and last 4-frame groups.  The output is bitwise the same either
- * way; turning it off makes every task compute all of its frames (the
- * streamed entry points always do).  sfe_extract_chunks_noalloc follows
- * the setting too.  Returns
+ * way; turning it off makes every task compute all of its frames.
+ * sfe_extract_chunks_noalloc and the streamed entry points follow the
+ * setting too.  Returns
  * SFE_INVALID_ARG for a null ctx. */
 int sfe_set_frame_sharing(sfe_ctx* ctx, int32_t enable);
 

@@ -335,14 +335,6 @@ int launch_pair(sfe_ctx* ctx, const Source& src, const Item* lm, const Item* d_l
   return SFE_OK;
 }
 
-// launch_pair over one table that both kernels read (items with their own
-// regions).
-int launch_own(sfe_ctx* ctx, const Source& src, const Item* items, const Item* d_items, int n, float* raw, void* out,
-               int32_t out_dtype, int pad_to, hipStream_t stream, int stages = kBoth, bool allow_timing = true) {
-  return launch_pair(ctx, src, items, d_items, n, items, d_items, n, raw, out, out_dtype, pad_to, stream, stages,
-                     allow_timing);
-}
-
 // The log-mel launch over table[0, n_lm): its grid, and whether its
 // first-item table (sfe::logmel_wave_items) fits kMaxLogmelWaves entries.
 struct WaveTable {
@@ -947,16 +939,14 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     int64_t tiles = 0;
     if ((rc = build_items(starts.data(), lens.data(), n, &items, frame_offsets, &tiles))) return rc;
 
-    // Group tasks into windows [wstart, wend) no longer than window_samples;
-    // items are re-based to the window and their tiles to the group.
+    // Group tasks into windows [wstart, wend) no longer than window_samples.
     struct Group {
       int32_t first, count;
       int64_t wstart, wend;
-      int32_t units, max_T;
     };
     std::vector<Group> groups;
     for (int32_t i = 0; i < n;) {
-      Group g{i, 0, items[i].start, items[i].start, 0, 0};
+      Group g{i, 0, items[i].start, items[i].start};
       while (i < n && items[i].start + items[i].len - g.wstart <= window_samples) {
         g.wend = std::max(g.wend, items[i].start + items[i].len);
         ++i;
@@ -969,8 +959,7 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     // buffer, so a window joins a batch only while that range stays within
     // batch_windows * window_samples samples and the gaps between
     // the batch's windows (copied but unused) add up to at most one window.
-    // Items are re-based to their half and their units numbered within the
-    // batch.
+    // Items are re-based to their half.
     struct Batch {
       size_t g0, g1;
       int64_t start, end;
@@ -994,25 +983,9 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     }
     for (size_t bi = 0; bi < batches.size(); ++bi) {
       const int64_t base = (int64_t)(bi & 1) * half - batches[bi].start;
-      int32_t t = 0;
-      for (size_t gi = batches[bi].g0; gi < batches[bi].g1; ++gi) {
-        Group& g = groups[gi];
-        const int32_t t0 = t;
-        for (int32_t i = g.first; i < g.first + g.count; ++i) {
-          items[i].start += base;
-          items[i].unit_off = t;
-          t += (int32_t)sfe::units_for(items[i].T);
-          g.max_T = std::max(g.max_T, (int)items[i].T);
-        }
-        g.units = t - t0;
-      }
+      for (size_t gi = batches[bi].g0; gi < batches[bi].g1; ++gi)
+        for (int32_t i = groups[gi].first; i < groups[gi].first + groups[gi].count; ++i) items[i].start += base;
     }
-    const size_t mbytes = items.size() * sizeof(Item);
-    ctx->meta_items.clear();  // the table uploaded below is re-based per window group
-    SFE_HIP(ctx->h_meta.reserve(mbytes));
-    SFE_HIP(ctx->meta.reserve(mbytes));
-    SFE_HIP(ctx->scratch.reserve((size_t)tiles * sfe::kRawTile * sizeof(float)));
-    float* raw = static_cast<float*>(ctx->scratch.ptr);
     // A recording already in pinned (page-locked) host memory is copied to
     // the device directly; pageable memory goes through two pinned staging
     // windows.
@@ -1029,17 +1002,9 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
     hipStream_t sc = ctx->s_compute, sx = ctx->s_copy;
     SFE_HIP(order_after_last(ctx, sc));
     SFE_HIP(order_after_last(ctx, sx));
-    memcpy(ctx->h_meta.ptr, items.data(), mbytes);
-    SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, sc));
-    SFE_HIP(hipEventRecord(ctx->h_meta.ev, sc));
-    ctx->h_meta.pending = true;
-    const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
     char* ring = static_cast<char*>(ctx->win.ptr);
-    Source rsrc = src;
-    rsrc.ptr = ring;
-    int32_t norm_first = 0;
-    size_t norm_windows = 0;  // windows featurized since the last normalisation
-    for (size_t bi = 0; bi < batches.size(); ++bi) {
+    // Batch bi's samples into half (bi & 1) of the ring, on the copy stream.
+    auto issue_copy = [&](size_t bi) -> int {
       const Batch& bt = batches[bi];
       const int e = (int)(bi & 1);
       // This half was last read by the log-mel launch of batch bi - 2.
@@ -1059,10 +1024,73 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
         ctx->h_win[e].pending = true;
       }
       SFE_HIP(hipEventRecord(ctx->ev_copied[e], sx));
+      return SFE_OK;
+    };
+    // The first batch's copy goes out before the host plans the tables.
+    if ((rc = issue_copy(0))) return rc;
+
+    // Per batch, the plan with shared frames (plan_table) over the batch's
+    // re-based items: frames that overlapping tasks of one batch share are
+    // computed once (tasks of different batches keep their own).  The
+    // batches' raw regions follow one another in the scratch; the table is
+    // every batch's log-mel entries, then every batch's normalisation
+    // entries (item order).
+    std::vector<Item> lm_tab, nm_tab;
+    std::vector<size_t> lm_at(batches.size() + 1, 0);
+    lm_tab.reserve(items.size());
+    nm_tab.reserve(items.size());
+    {
+      sfe::PlanWorkspace ws;
+      std::vector<Item> tbl;
+      int64_t raw_tiles = 0;
+      for (size_t bi = 0; bi < batches.size(); ++bi) {
+        const int32_t first = groups[batches[bi].g0].first;
+        const int32_t end = groups[batches[bi].g1 - 1].first + groups[batches[bi].g1 - 1].count;
+        const int nb = end - first;
+        ws.reserve((size_t)nb);
+        tbl.resize((size_t)(sfe::kPlanEntriesPerItem + 1) * (size_t)nb);
+        size_t n_lm = 0;
+        const int64_t bt_tiles = sfe::plan_table(items.data() + first, nb, ctx->share, &ws, tbl.data(), &n_lm);
+        const int64_t shift = (int64_t)sfe::kRawTile * raw_tiles;
+        for (size_t k = 0; k < n_lm + (size_t)nb; ++k) {
+          Item& e = tbl[k];
+          e.out_off += shift;
+          e.grid_off += shift;
+          e.tail_off += shift;
+          (k < n_lm ? lm_tab : nm_tab).push_back(e);
+        }
+        lm_at[bi + 1] = lm_tab.size();
+        raw_tiles += bt_tiles;
+      }
+      tiles = raw_tiles;
+    }
+    const size_t n_lm_all = lm_tab.size();
+    lm_tab.insert(lm_tab.end(), nm_tab.begin(), nm_tab.end());
+    const std::vector<Item>& table = lm_tab;  // log-mel entries, then normalisation entries
+    const size_t mbytes = table.size() * sizeof(Item);
+    ctx->meta_items.clear();  // the table uploaded below is re-based per window group
+    SFE_HIP(ctx->h_meta.reserve(mbytes));
+    SFE_HIP(ctx->meta.reserve(mbytes));
+    SFE_HIP(ctx->scratch.reserve((size_t)tiles * sfe::kRawTile * sizeof(float)));
+    float* raw = static_cast<float*>(ctx->scratch.ptr);
+    memcpy(ctx->h_meta.ptr, table.data(), mbytes);
+    SFE_HIP(hipMemcpyAsync(ctx->meta.ptr, ctx->h_meta.ptr, mbytes, hipMemcpyHostToDevice, sc));
+    SFE_HIP(hipEventRecord(ctx->h_meta.ev, sc));
+    ctx->h_meta.pending = true;
+    const Item* d_items = static_cast<const Item*>(ctx->meta.ptr);
+    Source rsrc = src;
+    rsrc.ptr = ring;
+    int32_t norm_first = 0;
+    size_t norm_windows = 0;  // windows featurized since the last normalisation
+    for (size_t bi = 0; bi < batches.size(); ++bi) {
+      const Batch& bt = batches[bi];
+      const int e = (int)(bi & 1);
+      if (bi > 0 && (rc = issue_copy(bi))) return rc;
       SFE_HIP(hipStreamWaitEvent(sc, ctx->ev_copied[e], 0));
-      const int32_t first = groups[bt.g0].first;
       const int32_t end = groups[bt.g1 - 1].first + groups[bt.g1 - 1].count;
-      rc = launch_own(ctx, rsrc, items.data() + first, d_items + first, end - first, raw, out, out_dtype, 0, sc,
+      const Item* lm = table.data() + lm_at[bi];
+      const int n_lm = (int)(lm_at[bi + 1] - lm_at[bi]);
+      rc = launch_pair(ctx, rsrc, lm, d_items + lm_at[bi], n_lm, nullptr, nullptr, 0, raw, out, out_dtype, 0, sc,
                        kLogmel);
       if (rc) return rc;
       SFE_HIP(hipEventRecord(ctx->ev_done[e], sc));
@@ -1071,7 +1099,8 @@ int sfe_extract_chunks_streamed_pcm(sfe_ctx* ctx, const void* host_recording, in
       // batch: one launch over many items instead of many launches over a few.
       norm_windows += bt.g1 - bt.g0;
       if (bi + 1 == batches.size() || norm_windows >= kStreamNormWindows) {
-        rc = launch_own(ctx, rsrc, items.data() + norm_first, d_items + norm_first, end - norm_first, raw, out,
+        const size_t nf = n_lm_all + (size_t)norm_first;
+        rc = launch_pair(ctx, rsrc, nullptr, nullptr, 0, table.data() + nf, d_items + nf, end - norm_first, raw, out,
                          out_dtype, 0, sc, kNorm);
         if (rc) return rc;
         norm_first = end;

@@ -727,6 +727,40 @@ def test_shared_frames_equal_own_frames(extractor, seed):
         assert_parity(g, oracle.extract(a), R.extract(a), R.f32_noise_envelope(a), what=f"task {i}")
 
 
+@pytest.mark.parametrize("window", [240_000, 700_000])
+def test_streamed_shared_frames_equal_own_frames(extractor, window):
+    """The streamed path shares frames among the overlapping tasks of one
+    batch of windows: random hop-aligned and unaligned tasks (ordered by
+    start, as the streamed entry point takes them, with duplicates and a
+    nested one) streamed with sharing on, streamed with sharing off and
+    featurized from HBM without sharing are bitwise the same."""
+    import torch
+    from scriptrs_amd import ChunkTask
+    _flush(f"case: streamed shared frames window={window}")
+    rng = np.random.default_rng(808)
+    rec = synth.speech_like(6_000_000, 808)
+    tasks = []
+    for _ in range(60):
+        n = int(rng.integers(1, 240_001))
+        s = int(rng.integers(0, (rec.size - n) // 160 + 1)) * 160 + int(rng.integers(0, 2)) * int(rng.integers(0, 160))
+        s = min(s, rec.size - n)
+        tasks.append(ChunkTask(s, s + n, s, 0))
+    tasks += tasks[:3] + [ChunkTask(tasks[7].audio_start + 1600, tasks[7].audio_start + 1600 + 30_000, 0, 0)]
+    tasks.sort(key=lambda t: t.audio_start)
+    try:
+        got = {}
+        for share in (True, False):
+            extractor.set_frame_sharing(share)
+            got[share] = extractor.extract_chunks_streamed(rec, tasks, window_samples=window)
+        own, fo = extractor.extract_chunks(torch.from_numpy(rec).cuda(), tasks)
+        torch.cuda.synchronize()
+    finally:
+        extractor.set_frame_sharing(True)
+    for share in (True, False):
+        assert np.array_equal(got[share][1], fo)
+        assert torch.equal(got[share][0], own), share
+
+
 def test_config3_shared_frames_equal_own_frames(extractor):
     """Config 3 at full size: the 280 chunks with their ~2 s overlaps
     computed once give bitwise the output of every chunk on its own."""
